@@ -1,0 +1,173 @@
+/*
+ * nva.h -- C ABI of the MI355X (gfx950) paged-attention library for nano-vllm-java.
+ *
+ * The library replaces the bodies of the reference's attention boundary:
+ *   RotaryEmbedding.forward(positions, q, k, ctx)   layers/Norms.java:275-346
+ *   Attention.forward(q, k, v, ctx)                  layers/Attention.java:152-171
+ * and owns the state those methods read:
+ *   KvCacheArena (per-layer K/V pages)               engine/KvCacheArena.java:63-142
+ *   Context.set (per-step varlen / paging metadata)  internal/Context.java:39-59
+ * (reference paths are relative to nano-vllm-java/src/main/java/com/igormaznitsa/nanollvm/).
+ *
+ * Conventions
+ *   - Every function returns an nva_status; 0 is success.  nva_last_error() returns the
+ *     message of the last failure on a context (the text the Java exception would carry).
+ *   - Tensor arguments (q, k, v, outputs) are DEVICE pointers to row-major fp32 arrays:
+ *     q/out [tokens, num_heads, head_dim], k/v [tokens, num_kv_heads, head_dim].
+ *     Step metadata (cu_seqlens, slots, tables, positions) are HOST pointers; they are copied
+ *     to the device once per nva_step_set() and shared by every layer of that step.
+ *   - All work is enqueued on the context's HIP stream and is asynchronous unless stated.
+ *   - A context is used by one host thread at a time (the reference's single generate thread,
+ *     Attention.java:41-44); there is no internal locking.
+ *   - There is no CPU fallback: nva_ctx_create() fails with NVA_E_HIP when no HIP device is
+ *     usable.
+ */
+#ifndef NVA_H
+#define NVA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t nva_status;
+
+enum {
+  NVA_OK = 0,
+  NVA_E_ARG = 1,        /* bad argument (Java: IllegalArgumentException) */
+  NVA_E_LAYER = 2,      /* layer index out of range, KvCacheArena.java:136-142 */
+  NVA_E_ROPE_POS = 3,   /* RoPE position outside [0, maxPos), Norms.java:318-322 */
+  NVA_E_SHARED_KV = 4,  /* shared-KV layer without slots or tables, Attention.java:189-191 */
+  NVA_E_NO_ARENA = 5,   /* no KV arena bound (Java: NullPointerException), Attention.java:153 */
+  NVA_E_NO_STEP = 6,    /* no step metadata set (Java: NullPointerException on Context) */
+  NVA_E_HIP = 7,        /* HIP runtime error or no usable device */
+  NVA_E_OOM = 8,        /* device or pinned allocation failed */
+  NVA_E_UNSUPPORTED = 9 /* shape this build has no kernel for (e.g. head_dim % 4 != 0) */
+};
+
+typedef struct nva_ctx nva_ctx;
+typedef struct nva_kv nva_kv;
+typedef struct nva_rope nva_rope;
+
+/* Constructor arguments of Attention(numHeads, headDim, scale, numKvHeads, slidingWindow,
+ * kvLayerIndex, writeKv), Attention.java:108-125.  sliding_window <= 0 means full context. */
+typedef struct nva_attn_desc {
+  int32_t num_heads;
+  int32_t head_dim;
+  float scale;
+  int32_t num_kv_heads;
+  int32_t sliding_window;
+  int32_t kv_layer_index;
+  int32_t write_kv;
+} nva_attn_desc;
+
+/* ------------------------------------------------------------------ context
+ * Replaces the per-LLM engine objects that Transformer builds and closes
+ * (engine/Transformer.java:113-143, 257-271). */
+nva_status nva_ctx_create(int device, nva_ctx **out);
+nva_status nva_ctx_destroy(nva_ctx *ctx);
+/* Use an external HIP stream (hipStream_t) for all later work; NULL restores the context's
+ * own stream.  The caller keeps the stream alive while it is set. */
+nva_status nva_ctx_set_stream(nva_ctx *ctx, void *hip_stream);
+void *nva_ctx_stream(nva_ctx *ctx);
+/* Blocks until all work enqueued on the context's stream has finished. */
+nva_status nva_ctx_sync(nva_ctx *ctx);
+const char *nva_last_error(nva_ctx *ctx);
+const char *nva_status_string(nva_status status);
+/* Per-kernel timing with HIP events on the context's stream (off by default).  Kernel names:
+ * "rope_store", "store", "decode", "merge", "prefill", "gather". */
+nva_status nva_ctx_set_timing(nva_ctx *ctx, int enable);
+nva_status nva_ctx_kernel_stats(nva_ctx *ctx, const char *kernel, int64_t *launches,
+                                double *total_ms);
+nva_status nva_ctx_reset_stats(nva_ctx *ctx);
+
+/* ------------------------------------------------------------------ KV arena
+ * KvCacheArena(numBlocks, blockSize, numKvHeads, headDims[], allocateLayer[]),
+ * KvCacheArena.java:63-90.  Each allocated layer owns zero-filled device buffers
+ * K and V of shape [num_blocks, block_size, num_kv_heads, head_dims[layer]] fp32 (slot s is
+ * block*block_size + offset, exactly the reference's layout).  allocate == NULL allocates every
+ * layer; allocate[i] == 0 gives that layer no pages (the reference's numel-1 dummy). */
+nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block_size,
+                         int num_kv_heads, const int32_t *head_dims, const uint8_t *allocate,
+                         nva_kv **out);
+/* KvCacheArena.close(), KvCacheArena.java:130-134: frees the device pages. */
+nva_status nva_kv_destroy(nva_kv *kv);
+/* getKeyCache/getValueCache(layer), KvCacheArena.java:111-124: device pointers and the byte
+ * size of each buffer (0 and NULL for an unallocated layer).  NVA_E_LAYER if out of range. */
+nva_status nva_kv_layer(nva_kv *kv, int layer, void **key, void **value, int64_t *bytes);
+/* Synchronous host<->device copies of a float range of one layer's K (which=0) or V
+ * (which=1) buffer, for callers that inspect or pre-fill pages (Tensor.data() access). */
+nva_status nva_kv_write(nva_kv *kv, int layer, int which, int64_t float_offset,
+                        const float *host, int64_t count);
+nva_status nva_kv_read(nva_kv *kv, int layer, int which, int64_t float_offset, float *host,
+                       int64_t count);
+
+/* ------------------------------------------------------------------ RoPE tables
+ * RotaryEmbedding's [maxPos, headSize] cos|sin table, Norms.java:171-191.
+ * nva_rope_create uploads the caller's own table (the Java table, so the bits are identical by
+ * construction); nva_rope_create_theta builds it on the host with the reference's arithmetic
+ * (invFreq = (float)(1/pow(base, 2i/d)); angle = (float)pos*invFreq as double; cos/sin cast to
+ * float), Norms.java:183-204. */
+nva_status nva_rope_create(nva_ctx *ctx, const float *cos_sin, int max_pos, int head_size,
+                           nva_rope **out);
+nva_status nva_rope_create_theta(nva_ctx *ctx, int head_size, int rotary_dim, int max_pos,
+                                 float base, nva_rope **out);
+nva_status nva_rope_destroy(nva_rope *rope);
+
+/* ------------------------------------------------------------------ step metadata
+ * Context.set(isPrefill, cuSeqlensQ, cuSeqlensK, maxSeqlenQ, maxSeqlenK, slotMapping,
+ * contextLens, blockTables, seqIds), Context.java:39-59, plus the step's positions tensor
+ * (Transformer.java:149-155).  Host arrays, copied to the device in one transfer:
+ *   cu_q, cu_k       [num_seqs+1]  prefill only (NULL for decode)
+ *   slot_mapping     [num_slots]   may be NULL (then the store is skipped, Attention.java:157)
+ *   context_lens     [num_seqs]    decode only (NULL for prefill)
+ *   block_tables     [num_seqs * bt_stride], -1 padded; NULL = no tables (dense prefill)
+ *   seq_ids          [num_tokens]  optional, kept for the caller
+ *   positions        [num_tokens]  fp32 positions, rounded like Math.round; may be NULL when
+ *                                  RoPE is not used this step
+ * For decode, num_seqs is the number of rows (one query token per sequence). */
+nva_status nva_step_set(nva_ctx *ctx, int is_prefill, const int32_t *cu_q, const int32_t *cu_k,
+                        int num_seqs, int max_seqlen_q, int max_seqlen_k,
+                        const int32_t *slot_mapping, int num_slots,
+                        const int32_t *context_lens, const int32_t *block_tables,
+                        int bt_stride, const int32_t *seq_ids, const float *positions,
+                        int num_tokens);
+/* Replaces the step's positions only (the positions tensor RotaryEmbedding.forward receives,
+ * Norms.java:275, rounded with Math.round as at Norms.java:317).  Valid after nva_step_set. */
+nva_status nva_step_positions(nva_ctx *ctx, const float *positions, int num_tokens);
+/* Context.clear(), Context.java:61-74. */
+nva_status nva_step_clear(nva_ctx *ctx);
+
+/* ------------------------------------------------------------------ compute
+ * RotaryEmbedding.forward(positions, q, k, ctx), Norms.java:275-346: q_out/k_out receive the
+ * rotated q [tokens, hq, d] and k [tokens, hk, d].  Positions come from nva_step_set().
+ * NVA_E_ROPE_POS if a rounded position is outside [0, max_pos) (no work is enqueued then). */
+nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, const float *k,
+                            int num_tokens, int hq, int hk, float *q_out, float *k_out);
+
+/* Attention.forward(q, k, v, ctx), Attention.java:152-171: store k/v into the layer's pages
+ * at the step's slots (when write_kv, the layer is allocated and num_slots == num_tokens;
+ * negative slots skipped), then dense prefill, paged prefill (block tables present) or
+ * decode, writing out [num_tokens, num_heads, head_dim].  Shared-KV layers (write_kv == 0)
+ * read layer kv_layer_index without storing. */
+nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
+                                 const float *q, const float *k, const float *v, int num_tokens,
+                                 float *out);
+
+/* The pair RotaryEmbedding.forward + Attention.forward as one call, the way the model layers
+ * use them (models/internal/Qwen3ForCausalLM.java:207-222): one fused kernel rotates q and k
+ * and stores rotated k and v into the pages, then the attention kernels run.  q_out/k_out
+ * may be NULL (context-owned scratch is used).  Results are identical to calling the two
+ * functions above in sequence. */
+nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                      const nva_attn_desc *desc, const float *q,
+                                      const float *k, const float *v, int num_tokens,
+                                      float *q_out, float *k_out, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVA_H */

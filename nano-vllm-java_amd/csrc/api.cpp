@@ -1,0 +1,1187 @@
+// C ABI of libnva.so: contexts, the device KV arena, per-step metadata upload, work planning
+// and the Attention.forward / RotaryEmbedding.forward dispatch.  See include/nva.h.
+//
+// Host-side restatements (reference paths relative to
+// nano-vllm-java/src/main/java/com/igormaznitsa/nanollvm/):
+//   Attention.forward dispatch and store rule   layers/Attention.java:152-171
+//   attendFromCache / gatherKvCache             layers/Attention.java:176-216
+//   kLen and query offsets per branch           layers/Attention.java:245-299, 353-358
+//   Math.round of positions and range check     layers/Norms.java:316-322
+//   RoPE table arithmetic                       layers/Norms.java:183-204
+//   KvCacheArena shapes and layer check         engine/KvCacheArena.java:63-142
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/nva.h"
+#include "nva_internal.h"
+
+using namespace nva;
+
+namespace {
+
+// Grow-only device buffer.
+struct DevBuf {
+  void *ptr = nullptr;
+  size_t cap = 0;
+  hipError_t reserve(size_t bytes) {
+    if (bytes <= cap) return hipSuccess;
+    if (ptr) {
+      hipError_t e = hipFree(ptr);
+      if (e != hipSuccess) return e;
+      ptr = nullptr;
+      cap = 0;
+    }
+    size_t want = std::max<size_t>(bytes, 4096);
+    hipError_t e = hipMalloc(&ptr, want);
+    if (e == hipSuccess) cap = want;
+    return e;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+};
+
+// Grow-only pinned host buffer whose last upload is tracked by an event, so it is only
+// overwritten once the device has consumed it.
+struct Staging {
+  void *ptr = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+  hipError_t wait() {
+    if (pending) {
+      pending = false;
+      return hipEventSynchronize(done);
+    }
+    return hipSuccess;
+  }
+  hipError_t reserve(size_t bytes) {
+    hipError_t e = wait();
+    if (e != hipSuccess) return e;
+    if (!done) {
+      e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+      if (e != hipSuccess) return e;
+    }
+    if (bytes <= cap) return hipSuccess;
+    if (ptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+    size_t want = std::max<size_t>(bytes, 4096);
+    e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
+    if (e == hipSuccess) cap = want;
+    return e;
+  }
+  hipError_t upload(DevBuf &dst, size_t bytes, hipStream_t s) {
+    hipError_t e = hipMemcpyAsync(dst.ptr, ptr, bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return e;
+    e = hipEventRecord(done, s);
+    if (e == hipSuccess) pending = true;
+    return e;
+  }
+  void release() {
+    if (pending) (void)hipEventSynchronize(done);
+    pending = false;
+    if (ptr) (void)hipHostFree(ptr);
+    if (done) (void)hipEventDestroy(done);
+    ptr = nullptr;
+    done = nullptr;
+    cap = 0;
+  }
+};
+
+// A work plan: the flattened row / merge / tile lists for one attention configuration of the
+// current step, built on the host and uploaded once, then reused by every layer with the same
+// configuration.
+struct PlanKey {
+  int window, mfma, tile_q, wg_per_item;
+  int tokens;                  // rows of q / out in the forward call
+  int paged;                   // keys through block tables (else dense k/v rows)
+  int block_size, num_blocks;  // arena geometry the tables are checked against
+  bool operator==(const PlanKey &o) const {
+    return window == o.window && mfma == o.mfma && tile_q == o.tile_q &&
+           wg_per_item == o.wg_per_item && tokens == o.tokens && paged == o.paged &&
+           block_size == o.block_size && num_blocks == o.num_blocks;
+  }
+};
+
+struct Plan {
+  PlanKey key{};
+  bool valid = false;
+  int num_rows = 0, num_merge = 0, num_tiles = 0, num_parts = 0;
+  bool covers_all = true;  // every output row is written by some kernel
+  size_t off_rows = 0, off_merge = 0, off_tiles = 0;
+  DevBuf dev;
+  Staging stage;
+};
+
+struct PendingTiming {
+  std::string name;
+  hipEvent_t start, stop;
+};
+
+struct KernelStat {
+  int64_t launches = 0;
+  double ms = 0.0;
+};
+
+}  // namespace
+
+struct nva_ctx {
+  int device = 0;
+  int num_cus = 256;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  std::string err;
+
+  // Step metadata (host copies) and its device mirror.
+  bool has_step = false;
+  bool is_prefill = false;
+  int num_seqs = 0;
+  int num_tokens = 0;
+  int max_q = 0, max_k = 0;
+  int bt_stride = 0;
+  int num_slots = 0;
+  int64_t slot_max = -1;  // largest slot of the step (negative slots are skipped)
+  bool has_cu = false, has_slots = false, has_ctx_lens = false, has_tables = false,
+       has_pos = false;
+  std::vector<int32_t> cu_q, cu_k, slots, ctx_lens, tables, seq_ids, pos;
+  DevBuf d_step;
+  Staging step_stage;
+  size_t off_cu_q = 0, off_cu_k = 0, off_slots = 0, off_ctx = 0, off_tables = 0, off_pos = 0;
+
+  std::vector<Plan *> plans;
+  DevBuf d_part;     // split partials
+  DevBuf d_q_rot;    // fused path scratch for rotated q
+  DevBuf d_k_rot;    // fused path scratch for rotated k
+  DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
+
+  bool timing = false;
+  std::vector<PendingTiming> pending;
+  std::vector<hipEvent_t> event_pool;
+  std::map<std::string, KernelStat> stats;
+
+  const int32_t *dev_i32(size_t off) const {
+    return reinterpret_cast<const int32_t *>(static_cast<char *>(d_step.ptr) + off);
+  }
+};
+
+struct nva_kv {
+  nva_ctx *ctx = nullptr;
+  int num_layers = 0, num_blocks = 0, block_size = 0, num_kv_heads = 0;
+  std::vector<int32_t> head_dims;
+  std::vector<float *> k, v;
+  std::vector<int64_t> bytes;
+};
+
+struct nva_rope {
+  nva_ctx *ctx = nullptr;
+  int max_pos = 0, head_size = 0;
+  float *table = nullptr;
+};
+
+namespace {
+
+nva_status fail(nva_ctx *ctx, nva_status st, const char *fmt, ...) {
+  if (ctx) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    ctx->err = buf;
+  }
+  return st;
+}
+
+nva_status hip_fail(nva_ctx *ctx, hipError_t e, const char *what) {
+  return fail(ctx, e == hipErrorOutOfMemory ? NVA_E_OOM : NVA_E_HIP, "%s: %s", what,
+              hipGetErrorString(e));
+}
+
+#define HIP_TRY(ctx, expr, what)                \
+  do {                                          \
+    hipError_t e_ = (expr);                     \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, what); \
+  } while (0)
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+hipEvent_t take_event(nva_ctx *ctx) {
+  if (!ctx->event_pool.empty()) {
+    hipEvent_t e = ctx->event_pool.back();
+    ctx->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets one kernel launch with timing events when timing is on.
+struct Timed {
+  nva_ctx *ctx;
+  const char *name;
+  hipEvent_t start = nullptr;
+  Timed(nva_ctx *c, const char *n) : ctx(c), name(n) {
+    if (ctx->timing) {
+      start = take_event(ctx);
+      if (start) (void)hipEventRecord(start, ctx->stream);
+    }
+  }
+  void done() {
+    if (!start) return;
+    hipEvent_t stop = take_event(ctx);
+    if (!stop) return;
+    (void)hipEventRecord(stop, ctx->stream);
+    ctx->pending.push_back({name, start, stop});
+    start = nullptr;
+  }
+};
+
+void resolve_timings(nva_ctx *ctx) {
+  for (auto &p : ctx->pending) {
+    float ms = 0.f;
+    if (hipEventSynchronize(p.stop) == hipSuccess &&
+        hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+      auto &s = ctx->stats[p.name];
+      s.launches++;
+      s.ms += ms;
+    }
+    ctx->event_pool.push_back(p.start);
+    ctx->event_pool.push_back(p.stop);
+  }
+  ctx->pending.clear();
+}
+
+int pow2_shift(int x) {
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < x) s++;
+  return s;
+}
+
+int largest_pow2_divisor_upto(int rep, int cap) {
+  int h = cap;
+  while (h > 1 && rep % h) h >>= 1;
+  return h;
+}
+
+// One query row of the row kernel before splitting.
+struct Row {
+  int qrow, seq, kbase, kbeg, kend;
+};
+
+// Builds (or reuses) the plan for this configuration of the current step.
+nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
+  for (Plan *p : ctx->plans)
+    if (p->valid && p->key == key) {
+      *out = p;
+      return NVA_OK;
+    }
+  Plan *plan = nullptr;
+  for (Plan *p : ctx->plans)
+    if (!p->valid) {
+      plan = p;
+      break;
+    }
+  if (!plan) {
+    plan = new Plan();
+    ctx->plans.push_back(plan);
+  }
+
+  const int W = key.window;
+  const bool paged = key.paged != 0;
+  std::vector<Row> rows;
+  std::vector<TileItem> tiles;
+  int covered = 0;
+  // Every page a sequence reads must be a real block of the arena: the reference would throw
+  // (ArrayIndexOutOfBounds) where a kernel would read out of bounds.
+  auto check_pages = [&](int b, int klen) -> nva_status {
+    if (klen <= 0) return NVA_OK;
+    const int pages = (int)(((int64_t)klen + key.block_size - 1) / key.block_size);
+    if (pages > ctx->bt_stride)
+      return fail(ctx, NVA_E_ARG, "sequence %d needs %d pages but its block table has %d", b,
+                  pages, ctx->bt_stride);
+    const int32_t *t = ctx->tables.data() + (size_t)b * ctx->bt_stride;
+    for (int j = 0; j < pages; j++)
+      if (t[j] < 0 || t[j] >= key.num_blocks)
+        return fail(ctx, NVA_E_ARG, "block table %d entry %d = %d is not a block in [0, %d)", b,
+                    j, t[j], key.num_blocks);
+    return NVA_OK;
+  };
+  if (!ctx->is_prefill) {
+    // Decode, Attention.java:285-299: row b, kLen = contextLens[b], absQ = kLen - 1.
+    const int n = key.tokens;
+    rows.reserve(n);
+    for (int b = 0; b < n; b++) {
+      const int klen = ctx->ctx_lens[b];
+      nva_status st = check_pages(b, klen);
+      if (st != NVA_OK) return st;
+      const int aq = klen - 1;
+      const int kbeg = W > 0 ? std::max(0, aq - W + 1) : 0;
+      rows.push_back({b, b, 0, kbeg, klen});
+    }
+    covered = n;
+  } else {
+    // Prefill, Attention.java:245-280: kLen = cuK[b+1]-cuK[b]; query qi at kLen-qLen+qi.
+    if (ctx->num_seqs > 0 && ctx->cu_q[ctx->num_seqs] > key.tokens)
+      return fail(ctx, NVA_E_ARG, "cuSeqlensQ ends at %d but q has %d rows",
+                  ctx->cu_q[ctx->num_seqs], key.tokens);
+    if (!paged && ctx->num_seqs > 0 && ctx->cu_k[ctx->num_seqs] > key.tokens)
+      return fail(ctx, NVA_E_ARG, "cuSeqlensK ends at %d but k has %d rows",
+                  ctx->cu_k[ctx->num_seqs], key.tokens);
+    for (int b = 0; b < ctx->num_seqs; b++) {
+      const int q0 = ctx->cu_q[b];
+      const int qlen = ctx->cu_q[b + 1] - q0;
+      const int klen = ctx->cu_k[b + 1] - ctx->cu_k[b];
+      const int kbase = paged ? 0 : ctx->cu_k[b];
+      if (qlen <= 0) continue;
+      if (paged) {
+        nva_status st = check_pages(b, klen);
+        if (st != NVA_OK) return st;
+      }
+      covered += qlen;
+      if (key.mfma && qlen >= 2 && klen >= qlen) {
+        for (int t0 = 0; t0 < qlen; t0 += key.tile_q) {
+          const int t1 = std::min(qlen, t0 + key.tile_q) - 1;
+          const int aq0 = klen - qlen + t0, aq1 = klen - qlen + t1;
+          TileItem ti;
+          ti.seq = b;
+          ti.qstart = q0;
+          ti.qlen = qlen;
+          ti.q0 = t0;
+          ti.klen = klen;
+          ti.kbase = kbase;
+          ti.ks = W > 0 ? std::max(0, aq0 - W + 1) : 0;
+          ti.ke = aq1 + 1;
+          tiles.push_back(ti);
+        }
+      } else {
+        for (int qi = 0; qi < qlen; qi++) {
+          const int aq = klen - qlen + qi;
+          const int kend = aq + 1;
+          const int kbeg = W > 0 ? std::max(0, aq - W + 1) : 0;
+          rows.push_back({q0 + qi, b, kbase, kbeg, kend});
+        }
+      }
+    }
+  }
+  plan->covers_all = covered == key.tokens;
+  // Longest tiles first: the grid is dispatched roughly in order, so this is an LPT schedule.
+  std::stable_sort(tiles.begin(), tiles.end(), [](const TileItem &a, const TileItem &b) {
+    return (a.ke - a.ks) > (b.ke - b.ks);
+  });
+
+  // Chunk: the largest of 1024..64 keys that still gives the grid >= 8 workgroups per CU.
+  int64_t total = 0;
+  for (const Row &r : rows) total += std::max(0, r.kend - r.kbeg);
+  const int64_t target = (int64_t)ctx->num_cus * 8;
+  int chunk = 64;
+  for (int c = 1024; c >= 64; c >>= 1) {
+    int64_t items = 0;
+    for (const Row &r : rows) {
+      const int len = r.kend - r.kbeg;
+      if (len > 0) items += (len + c - 1) / c;
+    }
+    if (items * key.wg_per_item >= target) {
+      chunk = c;
+      break;
+    }
+  }
+
+  std::vector<RowItem> items;
+  std::vector<MergeItem> merges;
+  items.reserve(rows.size() + total / chunk + 1);
+  int parts = 0;
+  for (const Row &r : rows) {
+    const int len = r.kend - r.kbeg;
+    if (len <= 0) {
+      merges.push_back({r.qrow, 0, 0, 0});
+      continue;
+    }
+    if (len <= chunk) {
+      items.push_back({r.qrow, r.seq, r.kbase, r.kbeg, r.kend, -1, 0, 0});
+      continue;
+    }
+    const int n = (len + chunk - 1) / chunk;
+    for (int j = 0; j < n; j++) {
+      const int b0 = r.kbeg + j * chunk;
+      const int b1 = std::min(r.kend, b0 + chunk);
+      items.push_back({r.qrow, r.seq, r.kbase, b0, b1, parts + j, 0, 0});
+    }
+    merges.push_back({r.qrow, parts, n, 0});
+    parts += n;
+  }
+
+  plan->key = key;
+  plan->num_rows = (int)items.size();
+  plan->num_merge = (int)merges.size();
+  plan->num_tiles = (int)tiles.size();
+  plan->num_parts = parts;
+  plan->off_rows = 0;
+  plan->off_merge = plan->off_rows + items.size() * sizeof(RowItem);
+  plan->off_tiles = plan->off_merge + merges.size() * sizeof(MergeItem);
+  const size_t bytes = plan->off_tiles + tiles.size() * sizeof(TileItem);
+  if (bytes > 0) {
+    HIP_TRY(ctx, plan->stage.reserve(bytes), "plan staging");
+    HIP_TRY(ctx, plan->dev.reserve(bytes), "plan buffer");
+    char *h = static_cast<char *>(plan->stage.ptr);
+    if (!items.empty()) memcpy(h + plan->off_rows, items.data(), items.size() * sizeof(RowItem));
+    if (!merges.empty())
+      memcpy(h + plan->off_merge, merges.data(), merges.size() * sizeof(MergeItem));
+    if (!tiles.empty()) memcpy(h + plan->off_tiles, tiles.data(), tiles.size() * sizeof(TileItem));
+    HIP_TRY(ctx, plan->stage.upload(plan->dev, bytes, ctx->stream), "plan upload");
+  }
+  plan->valid = true;
+  *out = plan;
+  return NVA_OK;
+}
+
+KvView make_paged_view(nva_ctx *ctx, nva_kv *kv, int layer) {
+  KvView v;
+  v.k = kv->k[layer];
+  v.v = kv->v[layer];
+  v.table = ctx->has_tables ? ctx->dev_i32(ctx->off_tables) : nullptr;
+  v.bt_stride = ctx->bt_stride;
+  v.block_size = kv->block_size;
+  v.bs_shift = pow2_shift(kv->block_size);
+  v.paged = 1;
+  return v;
+}
+
+KvView make_dense_view(const float *k, const float *v) {
+  KvView view;
+  view.k = k;
+  view.v = v;
+  view.table = nullptr;
+  view.bt_stride = 0;
+  view.block_size = 1;
+  view.bs_shift = 0;
+  view.paged = 0;
+  return view;
+}
+
+// The attention part of Attention.forward once the store (if any) is done.
+nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &view,
+                         int num_blocks, const float *q, int num_tokens, float *out) {
+  const int rep = d.num_heads / d.num_kv_heads;
+  const int hpw_row = largest_pow2_divisor_upto(rep, 8);
+  const int hpw_tile = largest_pow2_divisor_upto(rep, 4);
+  const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, hpw_tile);
+  if (!row_kernel_supports(d.head_dim, hpw_row))
+    return fail(ctx, NVA_E_UNSUPPORTED, "head_dim %d has no row kernel in this build",
+                d.head_dim);
+  PlanKey key;
+  key.window = d.sliding_window > 0 ? d.sliding_window : 0;
+  key.mfma = mfma ? 1 : 0;
+  key.tile_q = mfma ? prefill_tile_queries(hpw_tile) : 0;
+  key.wg_per_item = d.num_kv_heads * (rep / hpw_row);
+  key.tokens = num_tokens;
+  key.paged = view.paged;
+  key.block_size = view.paged ? view.block_size : 0;
+  key.num_blocks = view.paged ? num_blocks : 0;
+  Plan *plan = nullptr;
+  nva_status st = get_plan(ctx, key, &plan);
+  if (st != NVA_OK) return st;
+
+  if (!plan->covers_all) {
+    // Rows outside every sequence stay zero, as Tensor.zeros in the reference.
+    HIP_TRY(ctx, hipMemsetAsync(out, 0, (size_t)num_tokens * d.num_heads * d.head_dim * 4,
+                                ctx->stream),
+            "zero output");
+  }
+  char *pbase = static_cast<char *>(plan->dev.ptr);
+  if (plan->num_tiles > 0) {
+    TileLaunch t;
+    t.q = q;
+    t.out = out;
+    t.kv = view;
+    t.items = reinterpret_cast<const TileItem *>(pbase + plan->off_tiles);
+    t.num_items = plan->num_tiles;
+    t.hq = d.num_heads;
+    t.hkv = d.num_kv_heads;
+    t.head_dim = d.head_dim;
+    t.window = key.window;
+    t.scale = d.scale;
+    Timed tm(ctx, "prefill");
+    HIP_TRY(ctx, launch_prefill_tiles(t, hpw_tile, ctx->stream), "prefill kernel launch");
+    tm.done();
+  }
+  if (plan->num_rows > 0) {
+    const size_t parts = (size_t)plan->num_parts * d.num_heads;
+    const size_t need = parts * (2 + (size_t)d.head_dim) * sizeof(float);
+    HIP_TRY(ctx, ctx->d_part.reserve(need), "partial buffer");
+    float *pm = static_cast<float *>(ctx->d_part.ptr);
+    RowLaunch r;
+    r.q = q;
+    r.out = out;
+    r.kv = view;
+    r.items = reinterpret_cast<const RowItem *>(pbase + plan->off_rows);
+    r.num_items = plan->num_rows;
+    r.hq = d.num_heads;
+    r.hkv = d.num_kv_heads;
+    r.head_dim = d.head_dim;
+    r.scale = d.scale;
+    r.part_m = pm;
+    r.part_l = pm + parts;
+    r.part_acc = pm + 2 * parts;
+    Timed tm(ctx, "decode");
+    HIP_TRY(ctx, launch_row_attention(r, hpw_row, ctx->stream), "decode kernel launch");
+    tm.done();
+  }
+  if (plan->num_merge > 0) {
+    const size_t parts = (size_t)plan->num_parts * d.num_heads;
+    float *pm = static_cast<float *>(ctx->d_part.ptr);
+    MergeLaunch mg;
+    mg.out = out;
+    mg.items = reinterpret_cast<const MergeItem *>(pbase + plan->off_merge);
+    mg.num_items = plan->num_merge;
+    mg.hq = d.num_heads;
+    mg.head_dim = d.head_dim;
+    mg.part_m = pm;
+    mg.part_l = pm + parts;
+    mg.part_acc = pm + 2 * parts;
+    Timed tm(ctx, "merge");
+    HIP_TRY(ctx, launch_merge(mg, ctx->stream), "merge kernel launch");
+    tm.done();
+  }
+  return NVA_OK;
+}
+
+// Slots index the arena's num_blocks*block_size rows; the reference's arraycopy would throw
+// for a slot past the end.
+nva_status check_slots(nva_ctx *ctx, nva_kv *kv) {
+  const int64_t rows = (int64_t)kv->num_blocks * kv->block_size;
+  if (ctx->slot_max >= rows)
+    return fail(ctx, NVA_E_ARG, "slot %lld outside the arena's %lld slots",
+                (long long)ctx->slot_max, (long long)rows);
+  return NVA_OK;
+}
+
+nva_status check_positions(nva_ctx *ctx, int num_tokens, int max_pos) {
+  if (!ctx->has_pos) return fail(ctx, NVA_E_ARG, "the step has no positions");
+  if (num_tokens > (int)ctx->pos.size())
+    return fail(ctx, NVA_E_ARG, "%d tokens but the step has %d positions", num_tokens,
+                (int)ctx->pos.size());
+  for (int t = 0; t < num_tokens; t++) {
+    const int p = ctx->pos[t];
+    if (p < 0 || p >= max_pos)
+      return fail(ctx, NVA_E_ROPE_POS, "RoPE position %d out of range [0, %d)", p, max_pos);
+  }
+  return NVA_OK;
+}
+
+nva_status check_desc(nva_ctx *ctx, const nva_attn_desc *d) {
+  if (!d) return fail(ctx, NVA_E_ARG, "attention descriptor is null");
+  if (d->num_heads <= 0 || d->num_kv_heads <= 0 || d->head_dim <= 0)
+    return fail(ctx, NVA_E_ARG, "numHeads, numKvHeads and headDim must be > 0");
+  if (d->num_heads % d->num_kv_heads)
+    return fail(ctx, NVA_E_ARG, "numHeads %d is not a multiple of numKvHeads %d", d->num_heads,
+                d->num_kv_heads);
+  if (d->head_dim % 4) return fail(ctx, NVA_E_UNSUPPORTED, "headDim must be a multiple of 4");
+  return NVA_OK;
+}
+
+// Shared prologue of nva_attention_forward / nva_rope_attention_forward.
+nva_status check_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc, int num_tokens) {
+  nva_status st = check_desc(ctx, desc);
+  if (st != NVA_OK) return st;
+  if (!kv) return fail(ctx, NVA_E_NO_ARENA, "KV cache arena not bound in Context");
+  if (kv->ctx != ctx) return fail(ctx, NVA_E_ARG, "KV arena belongs to another context");
+  if (desc->kv_layer_index < 0 || desc->kv_layer_index >= kv->num_layers)
+    return fail(ctx, NVA_E_LAYER, "layerIndex out of range: %d (layers=%d)",
+                desc->kv_layer_index, kv->num_layers);
+  if (!ctx->has_step) return fail(ctx, NVA_E_NO_STEP, "no step metadata set on the context");
+  if (num_tokens < 0) return fail(ctx, NVA_E_ARG, "num_tokens < 0");
+  const int layer = desc->kv_layer_index;
+  if (kv->k[layer] && (kv->head_dims[layer] != desc->head_dim ||
+                       kv->num_kv_heads != desc->num_kv_heads))
+    return fail(ctx, NVA_E_ARG, "layer %d pages are [.., %d, %d], attention wants [.., %d, %d]",
+                layer, kv->num_kv_heads, kv->head_dims[layer], desc->num_kv_heads,
+                desc->head_dim);
+  if (!ctx->is_prefill) {
+    if (!ctx->has_ctx_lens || !ctx->has_tables)
+      return fail(ctx, NVA_E_ARG, "decode needs context lengths and block tables");
+    if (num_tokens > ctx->num_seqs)
+      return fail(ctx, NVA_E_ARG, "decode has %d rows but %d context lengths", num_tokens,
+                  ctx->num_seqs);
+  } else if (!ctx->has_cu) {
+    return fail(ctx, NVA_E_ARG, "prefill needs cu_seqlens");
+  }
+  return NVA_OK;
+}
+
+// Which K/V the attention reads, Attention.java:161-170 and :176-195.
+nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &d,
+                                 const float *q, const float *k, const float *v,
+                                 int num_tokens, float *out) {
+  const int layer = d.kv_layer_index;
+  const bool allocated = kv->k[layer] != nullptr;
+  if (ctx->is_prefill && !ctx->has_tables) {
+    if (d.write_kv) {
+      if (!k || !v) return fail(ctx, NVA_E_ARG, "dense prefill needs k and v");
+      return run_attention(ctx, d, make_dense_view(k, v), 0, q, num_tokens, out);
+    }
+    // Shared-KV dense prefill: gather the producer's rows at the step's slots.
+    if (!ctx->has_slots || ctx->num_slots != num_tokens)
+      return fail(ctx, NVA_E_SHARED_KV,
+                  "shared-KV attention needs slot mapping or block tables to read the "
+                  "producer cache");
+    if (!allocated) return fail(ctx, NVA_E_ARG, "producer layer %d has no pages", layer);
+    nva_status sst = check_slots(ctx, kv);
+    if (sst != NVA_OK) return sst;
+    const size_t row = (size_t)d.num_kv_heads * d.head_dim;
+    HIP_TRY(ctx, ctx->d_gather.reserve(2 * (size_t)num_tokens * row * 4 + 16), "gather buffer");
+    float *gk = static_cast<float *>(ctx->d_gather.ptr);
+    float *gv = gk + (size_t)num_tokens * row;
+    GatherLaunch g;
+    g.k_cache = kv->k[layer];
+    g.v_cache = kv->v[layer];
+    g.k_out = gk;
+    g.v_out = gv;
+    g.slots = ctx->dev_i32(ctx->off_slots);
+    g.tokens = num_tokens;
+    g.row = (int)row;
+    Timed tm(ctx, "gather");
+    HIP_TRY(ctx, launch_gather(g, ctx->stream), "gather kernel launch");
+    tm.done();
+    return run_attention(ctx, d, make_dense_view(gk, gv), 0, q, num_tokens, out);
+  }
+  if (!allocated) return fail(ctx, NVA_E_ARG, "layer %d has no pages to attend over", layer);
+  if (!ctx->has_tables) return fail(ctx, NVA_E_ARG, "paged attention needs block tables");
+  return run_attention(ctx, d, make_paged_view(ctx, kv, layer), kv->num_blocks, q,
+                       num_tokens, out);
+}
+
+// Math.round(float), Norms.java:317: floor(x + 1/2) evaluated exactly; NaN -> 0; saturating.
+int32_t java_round(float x) {
+  if (std::isnan(x)) return 0;
+  const float f = std::floor(x);
+  const float frac = x - f;
+  const double r = (double)f + (frac >= 0.5f ? 1.0 : 0.0);
+  if (r >= 2147483647.0) return 2147483647;
+  if (r <= -2147483648.0) return (-2147483647 - 1);
+  return (int32_t)r;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *nva_status_string(nva_status s) {
+  switch (s) {
+    case NVA_OK: return "ok";
+    case NVA_E_ARG: return "invalid argument";
+    case NVA_E_LAYER: return "layer index out of range";
+    case NVA_E_ROPE_POS: return "RoPE position out of range";
+    case NVA_E_SHARED_KV: return "shared-KV layer without slots or block tables";
+    case NVA_E_NO_ARENA: return "no KV arena";
+    case NVA_E_NO_STEP: return "no step metadata";
+    case NVA_E_HIP: return "HIP error";
+    case NVA_E_OOM: return "out of memory";
+    case NVA_E_UNSUPPORTED: return "unsupported shape";
+    default: return "unknown status";
+  }
+}
+
+nva_status nva_ctx_create(int device, nva_ctx **out) {
+  if (!out) return NVA_E_ARG;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return NVA_E_HIP;
+  if (device < 0 || device >= n) return NVA_E_ARG;
+  if (hipSetDevice(device) != hipSuccess) return NVA_E_HIP;
+  nva_ctx *ctx = new nva_ctx();
+  ctx->device = device;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+    ctx->num_cus = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
+    delete ctx;
+    return NVA_E_HIP;
+  }
+  ctx->stream = ctx->own_stream;
+  *out = ctx;
+  return NVA_OK;
+}
+
+nva_status nva_ctx_destroy(nva_ctx *ctx) {
+  if (!ctx) return NVA_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  resolve_timings(ctx);
+  for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+  for (Plan *p : ctx->plans) {
+    p->stage.release();
+    p->dev.release();
+    delete p;
+  }
+  ctx->step_stage.release();
+  ctx->d_step.release();
+  ctx->d_part.release();
+  ctx->d_q_rot.release();
+  ctx->d_k_rot.release();
+  ctx->d_gather.release();
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+  delete ctx;
+  return NVA_OK;
+}
+
+nva_status nva_ctx_set_stream(nva_ctx *ctx, void *hip_stream) {
+  if (!ctx) return NVA_E_ARG;
+  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+  return NVA_OK;
+}
+
+void *nva_ctx_stream(nva_ctx *ctx) { return ctx ? ctx->stream : nullptr; }
+
+nva_status nva_ctx_sync(nva_ctx *ctx) {
+  if (!ctx) return NVA_E_ARG;
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+  return NVA_OK;
+}
+
+const char *nva_last_error(nva_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+nva_status nva_ctx_set_timing(nva_ctx *ctx, int enable) {
+  if (!ctx) return NVA_E_ARG;
+  ctx->timing = enable != 0;
+  return NVA_OK;
+}
+
+nva_status nva_ctx_kernel_stats(nva_ctx *ctx, const char *kernel, int64_t *launches,
+                                double *total_ms) {
+  if (!ctx || !kernel) return NVA_E_ARG;
+  resolve_timings(ctx);
+  auto it = ctx->stats.find(kernel);
+  if (launches) *launches = it == ctx->stats.end() ? 0 : it->second.launches;
+  if (total_ms) *total_ms = it == ctx->stats.end() ? 0.0 : it->second.ms;
+  return NVA_OK;
+}
+
+nva_status nva_ctx_reset_stats(nva_ctx *ctx) {
+  if (!ctx) return NVA_E_ARG;
+  resolve_timings(ctx);
+  ctx->stats.clear();
+  return NVA_OK;
+}
+
+// ------------------------------------------------------------------------------- KV arena
+
+nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block_size,
+                         int num_kv_heads, const int32_t *head_dims, const uint8_t *allocate,
+                         nva_kv **out) {
+  if (!ctx || !out) return NVA_E_ARG;
+  *out = nullptr;
+  if (num_layers <= 0) return fail(ctx, NVA_E_ARG, "numLayers must be > 0");
+  if (num_blocks <= 0) return fail(ctx, NVA_E_ARG, "numBlocks must be > 0");
+  if (block_size <= 0 || num_kv_heads <= 0 || !head_dims)
+    return fail(ctx, NVA_E_ARG, "blockSize, numKvHeads must be > 0 and headDims non-null");
+  nva_kv *kv = new nva_kv();
+  kv->ctx = ctx;
+  kv->num_layers = num_layers;
+  kv->num_blocks = num_blocks;
+  kv->block_size = block_size;
+  kv->num_kv_heads = num_kv_heads;
+  kv->head_dims.assign(head_dims, head_dims + num_layers);
+  kv->k.assign(num_layers, nullptr);
+  kv->v.assign(num_layers, nullptr);
+  kv->bytes.assign(num_layers, 0);
+  (void)hipSetDevice(ctx->device);
+  for (int i = 0; i < num_layers; i++) {
+    if (allocate && !allocate[i]) continue;
+    if (head_dims[i] <= 0) {
+      nva_kv_destroy(kv);
+      return fail(ctx, NVA_E_ARG, "headDims[%d] must be > 0", i);
+    }
+    const int64_t bytes =
+        (int64_t)num_blocks * block_size * num_kv_heads * (int64_t)head_dims[i] * 4;
+    void *pk = nullptr, *pv = nullptr;
+    hipError_t e = hipMalloc(&pk, bytes);
+    if (e == hipSuccess) e = hipMalloc(&pv, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(pk, 0, bytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(pv, 0, bytes, ctx->stream);
+    if (e != hipSuccess) {
+      if (pk) (void)hipFree(pk);
+      if (pv) (void)hipFree(pv);
+      nva_kv_destroy(kv);
+      return hip_fail(ctx, e, "KV arena allocation");
+    }
+    kv->k[i] = static_cast<float *>(pk);
+    kv->v[i] = static_cast<float *>(pv);
+    kv->bytes[i] = bytes;
+  }
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "KV arena zero-fill");
+  *out = kv;
+  return NVA_OK;
+}
+
+nva_status nva_kv_destroy(nva_kv *kv) {
+  if (!kv) return NVA_OK;
+  if (kv->ctx) (void)hipStreamSynchronize(kv->ctx->stream);
+  for (size_t i = 0; i < kv->k.size(); i++) {
+    if (kv->k[i]) (void)hipFree(kv->k[i]);
+    if (kv->v[i]) (void)hipFree(kv->v[i]);
+  }
+  delete kv;
+  return NVA_OK;
+}
+
+nva_status nva_kv_layer(nva_kv *kv, int layer, void **key, void **value, int64_t *bytes) {
+  if (!kv) return NVA_E_ARG;
+  if (layer < 0 || layer >= kv->num_layers)
+    return fail(kv->ctx, NVA_E_LAYER, "layerIndex out of range: %d (layers=%d)", layer,
+                kv->num_layers);
+  if (key) *key = kv->k[layer];
+  if (value) *value = kv->v[layer];
+  if (bytes) *bytes = kv->bytes[layer];
+  return NVA_OK;
+}
+
+static nva_status kv_copy(nva_kv *kv, int layer, int which, int64_t off, void *host,
+                          int64_t count, bool to_device) {
+  if (!kv || !host || count < 0 || off < 0 || (which != 0 && which != 1)) return NVA_E_ARG;
+  nva_ctx *ctx = kv->ctx;
+  if (layer < 0 || layer >= kv->num_layers)
+    return fail(ctx, NVA_E_LAYER, "layerIndex out of range: %d (layers=%d)", layer,
+                kv->num_layers);
+  float *base = which == 0 ? kv->k[layer] : kv->v[layer];
+  if (!base) return fail(ctx, NVA_E_ARG, "layer %d has no pages", layer);
+  if ((off + count) * 4 > kv->bytes[layer])
+    return fail(ctx, NVA_E_ARG, "range [%lld, %lld) outside the layer's %lld floats",
+                (long long)off, (long long)(off + count), (long long)(kv->bytes[layer] / 4));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+  if (to_device)
+    HIP_TRY(ctx, hipMemcpy(base + off, host, count * 4, hipMemcpyHostToDevice), "KV write");
+  else
+    HIP_TRY(ctx, hipMemcpy(host, base + off, count * 4, hipMemcpyDeviceToHost), "KV read");
+  return NVA_OK;
+}
+
+nva_status nva_kv_write(nva_kv *kv, int layer, int which, int64_t float_offset,
+                        const float *host, int64_t count) {
+  return kv_copy(kv, layer, which, float_offset, const_cast<float *>(host), count, true);
+}
+
+nva_status nva_kv_read(nva_kv *kv, int layer, int which, int64_t float_offset, float *host,
+                       int64_t count) {
+  return kv_copy(kv, layer, which, float_offset, host, count, false);
+}
+
+// ------------------------------------------------------------------------------- RoPE tables
+
+nva_status nva_rope_create(nva_ctx *ctx, const float *cos_sin, int max_pos, int head_size,
+                           nva_rope **out) {
+  if (!ctx || !out || !cos_sin) return NVA_E_ARG;
+  *out = nullptr;
+  if (max_pos <= 0 || head_size <= 0 || head_size % 2)
+    return fail(ctx, NVA_E_ARG, "RoPE table needs maxPos > 0 and an even headSize");
+  const size_t bytes = (size_t)max_pos * head_size * 4;
+  void *p = nullptr;
+  HIP_TRY(ctx, hipMalloc(&p, bytes), "RoPE table allocation");
+  hipError_t e = hipMemcpy(p, cos_sin, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(ctx, e, "RoPE table upload");
+  }
+  nva_rope *r = new nva_rope();
+  r->ctx = ctx;
+  r->max_pos = max_pos;
+  r->head_size = head_size;
+  r->table = static_cast<float *>(p);
+  *out = r;
+  return NVA_OK;
+}
+
+nva_status nva_rope_create_theta(nva_ctx *ctx, int head_size, int rotary_dim, int max_pos,
+                                 float base, nva_rope **out) {
+  if (!ctx || !out) return NVA_E_ARG;
+  if (rotary_dim != head_size) return fail(ctx, NVA_E_ARG, "rotaryDim must equal headSize");
+  if (max_pos <= 0 || head_size <= 0 || head_size % 2)
+    return fail(ctx, NVA_E_ARG, "RoPE table needs maxPos > 0 and an even headSize");
+  const int half = head_size / 2;
+  std::vector<float> inv(half);
+  for (int i = 0; i < half; i++)
+    inv[i] = (float)(1.0 / std::pow((double)base, (2.0 * i) / rotary_dim));
+  std::vector<float> table((size_t)max_pos * head_size);
+  for (int pos = 0; pos < max_pos; pos++)
+    for (int i = 0; i < half; i++) {
+      volatile float prod = (float)pos * inv[i];  // float product, as in Java
+      const double freq = (double)prod;
+      table[(size_t)pos * head_size + i] = (float)std::cos(freq);
+      table[(size_t)pos * head_size + half + i] = (float)std::sin(freq);
+    }
+  return nva_rope_create(ctx, table.data(), max_pos, head_size, out);
+}
+
+nva_status nva_rope_destroy(nva_rope *rope) {
+  if (!rope) return NVA_OK;
+  if (rope->ctx) (void)hipStreamSynchronize(rope->ctx->stream);
+  if (rope->table) (void)hipFree(rope->table);
+  delete rope;
+  return NVA_OK;
+}
+
+// ------------------------------------------------------------------------------- step
+
+nva_status nva_step_set(nva_ctx *ctx, int is_prefill, const int32_t *cu_q, const int32_t *cu_k,
+                        int num_seqs, int max_seqlen_q, int max_seqlen_k,
+                        const int32_t *slot_mapping, int num_slots,
+                        const int32_t *context_lens, const int32_t *block_tables,
+                        int bt_stride, const int32_t *seq_ids, const float *positions,
+                        int num_tokens) {
+  if (!ctx) return NVA_E_ARG;
+  if (num_seqs < 0 || num_slots < 0 || num_tokens < 0 || bt_stride < 0)
+    return fail(ctx, NVA_E_ARG, "negative count in step metadata");
+  if (is_prefill && !cu_q) return fail(ctx, NVA_E_ARG, "prefill step needs cuSeqlensQ");
+  if (is_prefill && !cu_k) return fail(ctx, NVA_E_ARG, "prefill step needs cuSeqlensK");
+  if (block_tables && bt_stride <= 0 && num_seqs > 0)
+    return fail(ctx, NVA_E_ARG, "block tables need bt_stride > 0");
+  for (Plan *p : ctx->plans) p->valid = false;
+  ctx->has_step = true;
+  ctx->is_prefill = is_prefill != 0;
+  ctx->num_seqs = num_seqs;
+  ctx->num_tokens = num_tokens;
+  ctx->max_q = max_seqlen_q;
+  ctx->max_k = max_seqlen_k;
+  ctx->bt_stride = block_tables ? bt_stride : 0;
+  ctx->has_cu = cu_q && cu_k;
+  ctx->has_slots = slot_mapping != nullptr;
+  ctx->num_slots = slot_mapping ? num_slots : 0;
+  ctx->has_ctx_lens = context_lens != nullptr;
+  ctx->has_tables = block_tables != nullptr;
+  ctx->has_pos = positions != nullptr;
+  ctx->cu_q.assign(cu_q ? cu_q : nullptr, cu_q ? cu_q + num_seqs + 1 : nullptr);
+  ctx->cu_k.assign(cu_k ? cu_k : nullptr, cu_k ? cu_k + num_seqs + 1 : nullptr);
+  ctx->slots.assign(slot_mapping ? slot_mapping : nullptr,
+                    slot_mapping ? slot_mapping + num_slots : nullptr);
+  ctx->ctx_lens.assign(context_lens ? context_lens : nullptr,
+                       context_lens ? context_lens + num_seqs : nullptr);
+  ctx->tables.assign(block_tables ? block_tables : nullptr,
+                     block_tables ? block_tables + (size_t)num_seqs * bt_stride : nullptr);
+  ctx->seq_ids.assign(seq_ids ? seq_ids : nullptr, seq_ids ? seq_ids + num_tokens : nullptr);
+  ctx->slot_max = -1;
+  for (int32_t sl : ctx->slots) ctx->slot_max = std::max<int64_t>(ctx->slot_max, sl);
+  ctx->pos.resize(positions ? num_tokens : 0);
+  for (int t = 0; positions && t < num_tokens; t++) ctx->pos[t] = java_round(positions[t]);
+  if (ctx->is_prefill) {
+    for (int b = 0; b < num_seqs; b++)
+      if (cu_q[b + 1] < cu_q[b] || cu_k[b + 1] < cu_k[b]) {
+        ctx->has_step = false;
+        return fail(ctx, NVA_E_ARG, "cu_seqlens must be non-decreasing");
+      }
+  }
+
+  // One device blob: cu_q | cu_k | slots | ctx_lens | tables | positions (16-byte aligned).
+  auto align = [](size_t x) { return (x + 15) & ~(size_t)15; };
+  size_t off = 0;
+  ctx->off_cu_q = off;
+  off = align(off + ctx->cu_q.size() * 4);
+  ctx->off_cu_k = off;
+  off = align(off + ctx->cu_k.size() * 4);
+  ctx->off_slots = off;
+  off = align(off + ctx->slots.size() * 4);
+  ctx->off_ctx = off;
+  off = align(off + ctx->ctx_lens.size() * 4);
+  ctx->off_tables = off;
+  off = align(off + ctx->tables.size() * 4);
+  ctx->off_pos = off;
+  off = align(off + ctx->pos.size() * 4);
+  const size_t bytes = std::max<size_t>(off, 16);
+  (void)hipSetDevice(ctx->device);
+  HIP_TRY(ctx, ctx->step_stage.reserve(bytes), "step staging");
+  HIP_TRY(ctx, ctx->d_step.reserve(bytes), "step buffer");
+  char *h = static_cast<char *>(ctx->step_stage.ptr);
+  auto put = [&](size_t o, const std::vector<int32_t> &v) {
+    if (!v.empty()) memcpy(h + o, v.data(), v.size() * 4);
+  };
+  put(ctx->off_cu_q, ctx->cu_q);
+  put(ctx->off_cu_k, ctx->cu_k);
+  put(ctx->off_slots, ctx->slots);
+  put(ctx->off_ctx, ctx->ctx_lens);
+  put(ctx->off_tables, ctx->tables);
+  put(ctx->off_pos, ctx->pos);
+  HIP_TRY(ctx, ctx->step_stage.upload(ctx->d_step, bytes, ctx->stream), "step upload");
+  return NVA_OK;
+}
+
+nva_status nva_step_positions(nva_ctx *ctx, const float *positions, int num_tokens) {
+  if (!ctx) return NVA_E_ARG;
+  if (!ctx->has_step) return fail(ctx, NVA_E_NO_STEP, "no step metadata set on the context");
+  if (num_tokens < 0 || (num_tokens > 0 && !positions))
+    return fail(ctx, NVA_E_ARG, "positions required");
+  std::vector<int32_t> pos(num_tokens);
+  for (int t = 0; t < num_tokens; t++) pos[t] = java_round(positions[t]);
+  if (ctx->has_pos && pos == ctx->pos) return NVA_OK;
+  // Re-pack the step blob with the new positions at the end (the other arrays are unchanged).
+  ctx->pos.swap(pos);
+  ctx->has_pos = true;
+  const size_t bytes = std::max<size_t>(ctx->off_pos + ctx->pos.size() * 4, 16);
+  HIP_TRY(ctx, ctx->step_stage.reserve(bytes), "step staging");
+  // reserve() may have reallocated the staging buffer: rebuild its content completely.
+  char *h = static_cast<char *>(ctx->step_stage.ptr);
+  auto put = [&](size_t o, const std::vector<int32_t> &v) {
+    if (!v.empty()) memcpy(h + o, v.data(), v.size() * 4);
+  };
+  put(ctx->off_cu_q, ctx->cu_q);
+  put(ctx->off_cu_k, ctx->cu_k);
+  put(ctx->off_slots, ctx->slots);
+  put(ctx->off_ctx, ctx->ctx_lens);
+  put(ctx->off_tables, ctx->tables);
+  put(ctx->off_pos, ctx->pos);
+  if (ctx->d_step.cap < bytes) {
+    // A larger blob needs a new device buffer; plans only hold offsets, so they stay valid.
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "stream synchronize");
+    HIP_TRY(ctx, ctx->d_step.reserve(bytes), "step buffer");
+  }
+  HIP_TRY(ctx, ctx->step_stage.upload(ctx->d_step, bytes, ctx->stream), "step upload");
+  return NVA_OK;
+}
+
+nva_status nva_step_clear(nva_ctx *ctx) {
+  if (!ctx) return NVA_E_ARG;
+  ctx->has_step = false;
+  for (Plan *p : ctx->plans) p->valid = false;
+  return NVA_OK;
+}
+
+// ------------------------------------------------------------------------------- compute
+
+nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, const float *k,
+                            int num_tokens, int hq, int hk, float *q_out, float *k_out) {
+  if (!ctx) return NVA_E_ARG;
+  if (!rope) return fail(ctx, NVA_E_ARG, "RoPE table is null");
+  if (!ctx->has_step) return fail(ctx, NVA_E_NO_STEP, "no step metadata set on the context");
+  if (num_tokens < 0 || hq < 0 || hk < 0) return fail(ctx, NVA_E_ARG, "negative shape");
+  if (!q || !k || !q_out || !k_out) return fail(ctx, NVA_E_ARG, "q, k, q_out, k_out required");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(q_out) || !aligned16(k_out))
+    return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
+  nva_status st = check_positions(ctx, num_tokens, rope->max_pos);
+  if (st != NVA_OK) return st;
+  RopeStoreLaunch a{};
+  a.q = q;
+  a.k = k;
+  a.v = nullptr;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.k_cache = nullptr;
+  a.v_cache = nullptr;
+  a.slots = nullptr;
+  a.positions = ctx->dev_i32(ctx->off_pos);
+  a.cos_sin = rope->table;
+  a.tokens = num_tokens;
+  a.hq = hq;
+  a.hk = hk;
+  a.head_dim = rope->head_size;
+  Timed tm(ctx, "rope_store");
+  HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "rope kernel launch");
+  tm.done();
+  return NVA_OK;
+}
+
+nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
+                                 const float *q, const float *k, const float *v, int num_tokens,
+                                 float *out) {
+  if (!ctx) return NVA_E_ARG;
+  nva_status st = check_forward(ctx, kv, desc, num_tokens);
+  if (st != NVA_OK) return st;
+  if (!q || !out) return fail(ctx, NVA_E_ARG, "q and out are required");
+  if (!aligned16(q) || !aligned16(out) || (k && !aligned16(k)) || (v && !aligned16(v)))
+    return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
+  const nva_attn_desc d = *desc;
+  const int layer = d.kv_layer_index;
+  // Store first, Attention.java:157-160.
+  if (d.write_kv && kv->k[layer] && ctx->has_slots && ctx->num_slots == num_tokens &&
+      num_tokens > 0) {
+    if (!k || !v) return fail(ctx, NVA_E_ARG, "k and v are required to store");
+    st = check_slots(ctx, kv);
+    if (st != NVA_OK) return st;
+    RopeStoreLaunch a{};
+    a.q = nullptr;
+    a.k = k;
+    a.v = v;
+    a.k_cache = kv->k[layer];
+    a.v_cache = kv->v[layer];
+    a.slots = ctx->dev_i32(ctx->off_slots);
+    a.positions = nullptr;
+    a.tokens = num_tokens;
+    a.hq = d.num_heads;
+    a.hk = d.num_kv_heads;
+    a.head_dim = d.head_dim;
+    Timed tm(ctx, "store");
+    HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "store kernel launch");
+    tm.done();
+  }
+  return attention_after_store(ctx, kv, d, q, k, v, num_tokens, out);
+}
+
+nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                      const nva_attn_desc *desc, const float *q,
+                                      const float *k, const float *v, int num_tokens,
+                                      float *q_out, float *k_out, float *out) {
+  if (!ctx) return NVA_E_ARG;
+  nva_status st = check_forward(ctx, kv, desc, num_tokens);
+  if (st != NVA_OK) return st;
+  if (!rope) return fail(ctx, NVA_E_ARG, "RoPE table is null");
+  if (rope->head_size != desc->head_dim)
+    return fail(ctx, NVA_E_ARG, "RoPE head size %d != headDim %d", rope->head_size,
+                desc->head_dim);
+  if (!q || !k || !v || !out) return fail(ctx, NVA_E_ARG, "q, k, v and out are required");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
+      (q_out && !aligned16(q_out)) || (k_out && !aligned16(k_out)))
+    return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
+  st = check_positions(ctx, num_tokens, rope->max_pos);
+  if (st != NVA_OK) return st;
+  const nva_attn_desc d = *desc;
+  const int layer = d.kv_layer_index;
+  const size_t qn = (size_t)num_tokens * d.num_heads * d.head_dim;
+  const size_t kn = (size_t)num_tokens * d.num_kv_heads * d.head_dim;
+  if (!q_out) {
+    HIP_TRY(ctx, ctx->d_q_rot.reserve(qn * 4 + 16), "rotated q scratch");
+    q_out = static_cast<float *>(ctx->d_q_rot.ptr);
+  }
+  const bool dense = ctx->is_prefill && !ctx->has_tables;
+  if (!k_out && dense) {
+    HIP_TRY(ctx, ctx->d_k_rot.reserve(kn * 4 + 16), "rotated k scratch");
+    k_out = static_cast<float *>(ctx->d_k_rot.ptr);
+  }
+  const bool store = d.write_kv && kv->k[layer] && ctx->has_slots &&
+                     ctx->num_slots == num_tokens;
+  if (store) {
+    st = check_slots(ctx, kv);
+    if (st != NVA_OK) return st;
+  }
+  RopeStoreLaunch a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.k_cache = store ? kv->k[layer] : nullptr;
+  a.v_cache = store ? kv->v[layer] : nullptr;
+  a.slots = store ? ctx->dev_i32(ctx->off_slots) : nullptr;
+  a.positions = ctx->dev_i32(ctx->off_pos);
+  a.cos_sin = rope->table;
+  a.tokens = num_tokens;
+  a.hq = d.num_heads;
+  a.hk = d.num_kv_heads;
+  a.head_dim = d.head_dim;
+  {
+    Timed tm(ctx, "rope_store");
+    HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "rope_store kernel launch");
+    tm.done();
+  }
+  return attention_after_store(ctx, kv, d, q_out, k_out, v, num_tokens, out);
+}
+
+}  // extern "C"

@@ -1,0 +1,280 @@
+// Kernel (b): split-KV GQA/MQA attention of single query rows over the paged KV cache, and
+// the merge of split partials.
+//
+// Semantics (layers/Attention.java:285-299 decode, :328-396 attendJobs): query row r of head
+// h attends keys [kbeg, kend) of its sequence through the block table
+// (slot(t) = table[t / BS] * BS + t % BS, Attention.java:131-137) with the KV head
+// kvh = h / rep, score = dot(q, k) * scale, softmax over the keys, out = sum(w v) / sum(w),
+// and out = 0 when no key is visible.  The reference's 64-key online softmax is replaced by a
+// per-stream online softmax over 8-key groups and a final log-sum-exp merge of the streams;
+// the result agrees to fp32 rounding.
+//
+// Mapping onto CDNA4 (wave64):
+//   * one workgroup (4 waves) per (work item, KV head, group of HPW query heads); a work item
+//     is one query row and a chunk of its key range (the host splits long rows so that every
+//     workgroup reads about the same number of bytes and the grid has thousands of groups);
+//   * a K/V row (D fp32) is read by LPT = D/4 lanes as float4: each wave load instruction
+//     fetches TPW = 64/LPT whole rows, i.e. contiguous 128-byte lines, and all HPW query heads
+//     of the KV head reuse the registers (K/V are read from HBM exactly once per KV head);
+//   * the dot products are reduced across the LPT lanes with DPP row ops and one swizzle (no
+//     LDS traffic); each group of LPT lanes is an independent online-softmax stream;
+//   * the 4*TPW streams of the workgroup are merged through LDS at the end, and either the
+//     output row (unsplit item) or the partial (m, l, acc) of the chunk is written.
+// HBM bytes per work item: chunk * 2 * D * 4 per KV head (+ q, + the partial or output row).
+#include "nva_internal.h"
+
+namespace nva {
+
+namespace {
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_amdgcn_update_dpp(0.0f, x, CTRL, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ float swizzle_xor16(float x) {
+  // Bit-mode swizzle within 32-lane halves: and_mask 0x1F, or_mask 0, xor_mask 0x10.
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+}
+
+// Sum of x over aligned groups of LPT lanes; every lane of the group receives the sum.
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (LPT >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (LPT >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (LPT >= 8) x += dpp<0x141>(x);  // row_half_mirror
+  if constexpr (LPT >= 16) x += dpp<0x140>(x); // row_mirror
+  if constexpr (LPT >= 32) x += swizzle_xor16(x);
+  if constexpr (LPT >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ int64_t kv_row(const KvView &kv, const int32_t *table, int kbase,
+                                          int t) {
+  if (!kv.paged) return (int64_t)kbase + t;
+  int blk, off;
+  if (kv.bs_shift >= 0) {
+    blk = t >> kv.bs_shift;
+    off = t & (kv.block_size - 1);
+  } else {
+    blk = t / kv.block_size;
+    off = t - blk * kv.block_size;
+  }
+  return (int64_t)table[blk] * kv.block_size + off;
+}
+
+}  // namespace
+
+template <int D, int HPW>
+__global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
+  constexpr int LPT = D / 4;        // lanes per K/V row
+  constexpr int TPW = 64 / LPT;     // rows per wave load instruction
+  constexpr int U = 8;              // rows per stream per group
+  constexpr int G = TPW * U;        // rows per wave per group
+  constexpr int NS = 4 * TPW;       // softmax streams per workgroup
+  __shared__ float sm_m[NS][HPW];
+  __shared__ float sm_l[NS][HPW];
+  __shared__ float4 sm_acc[NS][HPW][LPT];
+
+  const RowItem it = a.items[blockIdx.x];
+  const int rep = a.hq / a.hkv;
+  const int groups = rep / HPW;
+  const int kvh = blockIdx.y / groups;
+  const int h0 = kvh * rep + (blockIdx.y - kvh * groups) * HPW;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / LPT;
+  const int c = lane - sub * LPT;
+
+  float4 qv[HPW];
+#pragma unroll
+  for (int h = 0; h < HPW; h++) qv[h] = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + c * 4);
+
+  const size_t rs = (size_t)a.hkv * D;
+  const float *kp = a.kv.k + (size_t)kvh * D + c * 4;
+  const float *vp = a.kv.v + (size_t)kvh * D + c * 4;
+  const int32_t *table = a.kv.paged ? a.kv.table + (size_t)it.seq * a.kv.bt_stride : nullptr;
+
+  float m[HPW], l[HPW];
+  float4 acc[HPW];
+#pragma unroll
+  for (int h = 0; h < HPW; h++) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+    acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  for (int g0 = it.kbeg + wave * G; g0 < it.kend; g0 += 4 * G) {
+    float4 kr[U], vr[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int t = g0 + u * TPW + sub;
+      ok[u] = t < it.kend;
+      const int64_t row = kv_row(a.kv, table, it.kbase, ok[u] ? t : it.kbeg);
+      kr[u] = ld4(kp + row * rs);
+      vr[u] = ld4(vp + row * rs);
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; h++) {
+      float s[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        float p = qv[h].x * kr[u].x;
+        p = fmaf(qv[h].y, kr[u].y, p);
+        p = fmaf(qv[h].z, kr[u].z, p);
+        p = fmaf(qv[h].w, kr[u].w, p);
+        s[u] = group_sum<LPT>(p);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        s[u] = ok[u] ? s[u] * a.scale : -INFINITY;
+        mx = fmaxf(mx, s[u]);
+      }
+      const float mn = fmaxf(m[h], mx);
+      const float ms = mn == -INFINITY ? 0.0f : mn;
+      const float alpha = expf(m[h] - ms);
+      float ls = 0.0f;
+      float4 av = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const float w = expf(s[u] - ms);
+        ls += w;
+        av.x = fmaf(w, vr[u].x, av.x);
+        av.y = fmaf(w, vr[u].y, av.y);
+        av.z = fmaf(w, vr[u].z, av.z);
+        av.w = fmaf(w, vr[u].w, av.w);
+      }
+      l[h] = fmaf(l[h], alpha, ls);
+      acc[h].x = fmaf(acc[h].x, alpha, av.x);
+      acc[h].y = fmaf(acc[h].y, alpha, av.y);
+      acc[h].z = fmaf(acc[h].z, alpha, av.z);
+      acc[h].w = fmaf(acc[h].w, alpha, av.w);
+      m[h] = mn;
+    }
+  }
+
+  const int stream = wave * TPW + sub;
+#pragma unroll
+  for (int h = 0; h < HPW; h++) {
+    if (c == 0) {
+      sm_m[stream][h] = m[h];
+      sm_l[stream][h] = l[h];
+    }
+    sm_acc[stream][h][c] = acc[h];
+  }
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < HPW * LPT; idx += blockDim.x) {
+    const int h = idx / LPT;
+    const int cc = idx - h * LPT;
+    float M = -INFINITY;
+    for (int s = 0; s < NS; s++) M = fmaxf(M, sm_m[s][h]);
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < NS; s++) {
+      const float e = expf(sm_m[s][h] - Ms);
+      L = fmaf(sm_l[s][h], e, L);
+      const float4 x = sm_acc[s][h][cc];
+      A.x = fmaf(x.x, e, A.x);
+      A.y = fmaf(x.y, e, A.y);
+      A.z = fmaf(x.z, e, A.z);
+      A.w = fmaf(x.w, e, A.w);
+    }
+    if (it.part < 0) {
+      const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+      st4(a.out + ((size_t)it.qrow * a.hq + h0 + h) * D + cc * 4,
+          make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv));
+    } else {
+      const size_t p = (size_t)it.part * a.hq + h0 + h;
+      st4(a.part_acc + p * D + cc * 4, A);
+      if (cc == 0) {
+        a.part_m[p] = M;
+        a.part_l[p] = L;
+      }
+    }
+  }
+}
+
+// Log-sum-exp merge of the chunk partials of split rows; rows with no visible key get zeros.
+__global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
+  const MergeItem it = a.items[blockIdx.x];
+  const int d4 = a.head_dim >> 2;
+  for (int idx = threadIdx.x; idx < a.hq * d4; idx += blockDim.x) {
+    const int h = idx / d4;
+    const int cc = idx - h * d4;
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (it.nparts > 0) {
+      float M = -INFINITY;
+      for (int p = 0; p < it.nparts; p++) M = fmaxf(M, a.part_m[(size_t)(it.first + p) * a.hq + h]);
+      const float Ms = M == -INFINITY ? 0.0f : M;
+      float L = 0.0f;
+      float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int p = 0; p < it.nparts; p++) {
+        const size_t pi = (size_t)(it.first + p) * a.hq + h;
+        const float e = expf(a.part_m[pi] - Ms);
+        L = fmaf(a.part_l[pi], e, L);
+        const float4 x = ld4(a.part_acc + pi * a.head_dim + cc * 4);
+        A.x = fmaf(x.x, e, A.x);
+        A.y = fmaf(x.y, e, A.y);
+        A.z = fmaf(x.z, e, A.z);
+        A.w = fmaf(x.w, e, A.w);
+      }
+      const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+      r = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+    }
+    st4(a.out + ((size_t)it.qrow * a.hq + h) * a.head_dim + cc * 4, r);
+  }
+}
+
+namespace {
+
+template <int D>
+hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
+  const dim3 grid(a.num_items, a.hkv * ((a.hq / a.hkv) / hpw));
+  switch (hpw) {
+    case 1: hipLaunchKernelGGL((row_attention_kernel<D, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((row_attention_kernel<D, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((row_attention_kernel<D, 4>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((row_attention_kernel<D, 8>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool row_kernel_supports(int head_dim, int heads_per_wg) {
+  const bool d_ok = head_dim == 4 || head_dim == 8 || head_dim == 16 || head_dim == 32 ||
+                    head_dim == 64 || head_dim == 128 || head_dim == 256;
+  const bool h_ok = heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 ||
+                    heads_per_wg == 8;
+  return d_ok && h_ok;
+}
+
+hipError_t launch_row_attention(const RowLaunch &a, int hpw, hipStream_t s) {
+  if (a.num_items <= 0) return hipSuccess;
+  switch (a.head_dim) {
+    case 4: return launch_row_d<4>(a, hpw, s);
+    case 8: return launch_row_d<8>(a, hpw, s);
+    case 16: return launch_row_d<16>(a, hpw, s);
+    case 32: return launch_row_d<32>(a, hpw, s);
+    case 64: return launch_row_d<64>(a, hpw, s);
+    case 128: return launch_row_d<128>(a, hpw, s);
+    case 256: return launch_row_d<256>(a, hpw, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_merge(const MergeLaunch &a, hipStream_t s) {
+  if (a.num_items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(merge_kernel, dim3(a.num_items), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace nva

@@ -1,0 +1,116 @@
+// Internal declarations shared by the C-ABI host code and the HIP kernels of libnva.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nva {
+
+// One unit of the row kernel: one query row attending over the key range [kbeg, kend) of one
+// sequence.  Decode rows, qLen == 1 prefill rows and the prefill fallback all use it.  A
+// row whose key range is split produces partial (m, l, acc) results at index `part`; an
+// unsplit row (part < 0) writes its output directly.
+struct RowItem {
+  int32_t qrow;   // row of q / out ([T, Hq, D])
+  int32_t seq;    // block-table row (paged K/V)
+  int32_t kbase;  // dense K/V: row of key 0 in k/v ([T, Hkv, D]); paged: unused
+  int32_t kbeg;   // first key (absolute position in the sequence)
+  int32_t kend;   // one past the last key
+  int32_t part;   // partial-result slot, or -1
+  int32_t pad0, pad1;
+};
+
+// Combines the partials of one split row (nparts >= 2) or zero-fills a row with no visible
+// key (nparts == 0), as Attention.java:393-394 gives 0 when l == 0.
+struct MergeItem {
+  int32_t qrow;
+  int32_t first;
+  int32_t nparts;
+  int32_t pad;
+};
+
+// One workgroup of the MFMA prefill kernel: a tile of queries of one sequence, for one KV
+// head (and a group of its query heads), over the key tiles [ks, ke).
+struct TileItem {
+  int32_t seq;     // block-table row (paged) / sequence index
+  int32_t qstart;  // row of the sequence's first query in q/out
+  int32_t qlen;    // queries of the sequence
+  int32_t q0;      // first query of this tile (index within the sequence)
+  int32_t klen;    // keys of the sequence (kLen in the reference)
+  int32_t kbase;   // dense K/V: row of key 0; paged: unused
+  int32_t ks;      // first key any query of the tile sees
+  int32_t ke;      // one past the last key any query of the tile sees
+};
+
+struct KvView {
+  const float *k;        // paged: cache base; dense: k input base
+  const float *v;
+  const int32_t *table;  // block tables (paged) or nullptr (dense)
+  int32_t bt_stride;
+  int32_t block_size;
+  int32_t bs_shift;      // log2(block_size) when a power of two, else -1
+  int32_t paged;
+};
+
+struct RowLaunch {
+  const float *q;
+  float *out;
+  KvView kv;
+  const RowItem *items;
+  int32_t num_items;
+  int32_t hq, hkv, head_dim;
+  float scale;
+  float *part_m, *part_l, *part_acc;  // [P, Hq], [P, Hq], [P, Hq, D]
+};
+
+struct MergeLaunch {
+  float *out;
+  const MergeItem *items;
+  int32_t num_items;
+  int32_t hq, head_dim;
+  const float *part_m, *part_l, *part_acc;
+};
+
+struct TileLaunch {
+  const float *q;
+  float *out;
+  KvView kv;
+  const TileItem *items;
+  int32_t num_items;
+  int32_t hq, hkv, head_dim;
+  int32_t window;  // 0 = none
+  float scale;
+};
+
+struct RopeStoreLaunch {
+  const float *q, *k, *v;     // inputs [T, hq, d], [T, hk, d], [T, hk, d]; k/v may be null
+  float *q_out, *k_out;       // rotated outputs (k_out may be null)
+  float *k_cache, *v_cache;   // store targets (null: no store)
+  const int32_t *slots;       // [T] or null
+  const int32_t *positions;   // [T] rounded, validated positions (null: no rotation)
+  const float *cos_sin;       // [max_pos, d]
+  int32_t tokens, hq, hk, head_dim;
+};
+
+struct GatherLaunch {
+  const float *k_cache, *v_cache;
+  float *k_out, *v_out;       // [T, hk, d]
+  const int32_t *slots;
+  int32_t tokens, row;        // row = hk * d floats
+};
+
+// Kernel launchers (each returns the hipGetLastError() of its launch).
+hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s);
+hipError_t launch_gather(const GatherLaunch &a, hipStream_t s);
+hipError_t launch_row_attention(const RowLaunch &a, int heads_per_wg, hipStream_t s);
+hipError_t launch_merge(const MergeLaunch &a, hipStream_t s);
+hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream_t s);
+
+// Shapes the kernels are instantiated for.
+bool row_kernel_supports(int head_dim, int heads_per_wg);
+bool prefill_kernel_supports(int head_dim, int heads_per_wg);
+
+// Query rows per prefill workgroup for a given heads-per-workgroup choice.
+inline int prefill_tile_queries(int heads_per_wg) { return 32 * (4 / heads_per_wg); }
+
+}  // namespace nva

@@ -1,0 +1,402 @@
+"""Host-side mirror of nano-vllm-java's attention boundary over libnva.so.
+
+Class and method names follow the reference so that callers (and the parity tests) read like
+the reference's own code:
+
+* ``Context``        -- internal/Context.java (step metadata; ``set``/``clear``) plus the device
+                        and stream the native context owns.
+* ``KvCacheArena``   -- engine/KvCacheArena.java (per-layer K/V pages, resident in HBM).
+* ``RotaryEmbedding``-- layers/Norms.java:158-388 (cos|sin table, ``forward``).
+* ``Attention``      -- layers/Attention.java (constructor arguments, ``forward``).
+
+(Reference paths are relative to nano-vllm-java/src/main/java/com/igormaznitsa/nanollvm/.)
+Tensors are torch CUDA float32 tensors (device memory only; torch does no compute here).  Java
+exceptions map to Python exceptions of the same names.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native as N
+
+
+class NvaError(RuntimeError):
+    """Any failure reported by libnva.so."""
+
+
+class IllegalArgumentException(NvaError, ValueError):
+    pass
+
+
+class IllegalStateException(NvaError):
+    pass
+
+
+class NullPointerException(NvaError, TypeError):
+    pass
+
+
+class UnsupportedShapeError(NvaError, NotImplementedError):
+    pass
+
+
+_EXC = {
+    N.NVA_E_ARG: IllegalArgumentException,
+    N.NVA_E_LAYER: IllegalArgumentException,
+    N.NVA_E_ROPE_POS: IllegalArgumentException,
+    N.NVA_E_SHARED_KV: IllegalStateException,
+    N.NVA_E_NO_ARENA: NullPointerException,
+    N.NVA_E_NO_STEP: NullPointerException,
+    N.NVA_E_UNSUPPORTED: UnsupportedShapeError,
+}
+
+
+def _check(ctx_handle, status: int, what: str) -> None:
+    if status == N.NVA_OK:
+        return
+    lib = N.load()
+    msg = lib.nva_last_error(ctx_handle) if ctx_handle else None
+    msg = msg.decode() if msg else lib.nva_status_string(status).decode()
+    raise _EXC.get(status, NvaError)(f"{what}: {msg}")
+
+
+def _i32(a) -> Optional[np.ndarray]:
+    if a is None:
+        return None
+    return np.ascontiguousarray(np.asarray(a), dtype=np.int32)
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+def _dev(t: Optional[torch.Tensor], name: str):
+    if t is None:
+        return None
+    if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+        raise IllegalArgumentException(f"{name} must be a contiguous float32 device tensor")
+    return t.data_ptr()
+
+
+class Context:
+    """Context.java plus the native context (device, stream, step buffers).
+
+    ``stream`` defaults to torch's current stream on the device so that the library's kernels
+    are ordered with the caller's torch work."""
+
+    def __init__(self, device: int = 0, stream: Optional[torch.cuda.Stream] = None):
+        lib = N.load()
+        h = ctypes.c_void_p()
+        st = lib.nva_ctx_create(device, ctypes.byref(h))
+        if st != N.NVA_OK:
+            raise NvaError(f"nva_ctx_create(device={device}) failed: "
+                           f"{lib.nva_status_string(st).decode()} (no usable HIP device?)")
+        self._h = h
+        self.device = device
+        self._kv = None
+        self._positions_key = None
+        s = stream if stream is not None else torch.cuda.current_stream(device)
+        _check(self._h, lib.nva_ctx_set_stream(self._h, ctypes.c_void_p(s.cuda_stream)),
+               "set_stream")
+        self._stream = s
+
+    @property
+    def handle(self):
+        return self._h
+
+    # ---- Context.java API
+    def bind_kv_cache(self, arena: "KvCacheArena") -> None:
+        self._kv = arena
+
+    def kv_cache(self) -> Optional["KvCacheArena"]:
+        return self._kv
+
+    def set(self, is_prefill: bool, cu_seqlens_q=None, cu_seqlens_k=None, max_seqlen_q: int = 0,
+            max_seqlen_k: int = 0, slot_mapping=None, context_lens=None, block_tables=None,
+            seq_ids=None, positions=None) -> None:
+        """Context.set (Context.java:39-59); ``block_tables`` is a list of per-sequence lists or
+        a 2-D array, padded with -1 (Transformer.prepareBlockTables); ``positions`` is the
+        step's float positions tensor."""
+        cu_q, cu_k = _i32(cu_seqlens_q), _i32(cu_seqlens_k)
+        slots = _i32(slot_mapping)
+        lens = _i32(context_lens)
+        bt = None
+        stride = 0
+        if block_tables is not None:
+            if isinstance(block_tables, np.ndarray):
+                bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+            else:
+                width = max((len(r) for r in block_tables), default=0)
+                bt = np.full((len(block_tables), max(width, 1)), -1, np.int32)
+                for i, r in enumerate(block_tables):
+                    bt[i, :len(r)] = r
+            if bt.ndim != 2:
+                raise IllegalArgumentException("block tables must be 2-D")
+            if bt.shape[1] == 0:
+                bt = np.full((bt.shape[0], 1), -1, np.int32)
+            stride = bt.shape[1]
+        if is_prefill:
+            num_seqs = 0 if cu_q is None else len(cu_q) - 1
+        else:
+            num_seqs = 0 if lens is None else len(lens)
+        ids = _i32(seq_ids)
+        pos = None if positions is None else np.ascontiguousarray(
+            positions.detach().cpu().numpy() if isinstance(positions, torch.Tensor) else positions,
+            dtype=np.float32)
+        ntok = len(pos) if pos is not None else (len(ids) if ids is not None else 0)
+        lib = N.load()
+        _check(self._h, lib.nva_step_set(
+            self._h, int(bool(is_prefill)), _ptr(cu_q), _ptr(cu_k), num_seqs, int(max_seqlen_q),
+            int(max_seqlen_k), _ptr(slots), 0 if slots is None else len(slots), _ptr(lens),
+            _ptr(bt), stride, _ptr(ids), _ptr(pos), ntok), "Context.set")
+        self._positions_key = None if pos is None else pos.tobytes()
+
+    def set_positions(self, positions) -> None:
+        pos = np.ascontiguousarray(
+            positions.detach().cpu().numpy() if isinstance(positions, torch.Tensor) else positions,
+            dtype=np.float32)
+        key = pos.tobytes()
+        if key == self._positions_key:
+            return
+        lib = N.load()
+        _check(self._h, lib.nva_step_positions(self._h, _ptr(pos), len(pos)), "positions")
+        self._positions_key = key
+
+    def clear(self) -> None:
+        N.load().nva_step_clear(self._h)
+        self._kv = None
+        self._positions_key = None
+
+    # ---- native extras
+    def sync(self) -> None:
+        _check(self._h, N.load().nva_ctx_sync(self._h), "sync")
+
+    def set_timing(self, enable: bool) -> None:
+        _check(self._h, N.load().nva_ctx_set_timing(self._h, int(bool(enable))), "timing")
+
+    def kernel_stats(self, kernel: str):
+        n = ctypes.c_int64()
+        ms = ctypes.c_double()
+        _check(self._h, N.load().nva_ctx_kernel_stats(self._h, kernel.encode(), ctypes.byref(n),
+                                                        ctypes.byref(ms)), "kernel_stats")
+        return n.value, ms.value
+
+    def reset_stats(self) -> None:
+        _check(self._h, N.load().nva_ctx_reset_stats(self._h), "reset_stats")
+
+    def close(self) -> None:
+        if self._h:
+            N.load().nva_ctx_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class KvCacheArena:
+    """KvCacheArena(numLayers, numBlocks, blockSize, numKvHeads, headDim) or, with per-layer
+    ``head_dims``/``allocate``, KvCacheArena(numBlocks, blockSize, numKvHeads, headDims[],
+    allocateLayer[]) (KvCacheArena.java:41-90).  Pages live in HBM, zero-filled."""
+
+    def __init__(self, ctx: Context, num_layers: int, num_blocks: int, block_size: int,
+                 num_kv_heads: int, head_dim: int = 0, head_dims: Sequence[int] = None,
+                 allocate: Sequence[bool] = None):
+        if head_dims is None:
+            head_dims = [head_dim] * num_layers
+        if allocate is None:
+            allocate = [True] * len(head_dims)
+        if len(head_dims) != len(allocate):
+            raise IllegalArgumentException("headDims and allocateLayer length mismatch")
+        hd = np.asarray(head_dims, np.int32)
+        al = np.asarray([1 if a else 0 for a in allocate], np.uint8)
+        h = ctypes.c_void_p()
+        lib = N.load()
+        _check(ctx.handle, lib.nva_kv_create(ctx.handle, len(hd), num_blocks, block_size,
+                                             num_kv_heads, _ptr(hd), _ptr(al), ctypes.byref(h)),
+               "KvCacheArena")
+        self._h = h
+        self._ctx = ctx
+        self.num_layers = len(hd)
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_kv_heads = num_kv_heads
+        self.head_dims = list(head_dims)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def _layer(self, layer: int):
+        k = ctypes.c_void_p()
+        v = ctypes.c_void_p()
+        n = ctypes.c_int64()
+        _check(self._ctx.handle, N.load().nva_kv_layer(self._h, layer, ctypes.byref(k),
+                                                       ctypes.byref(v), ctypes.byref(n)),
+               "KvCacheArena layer")
+        return k.value, v.value, n.value
+
+    def shape(self, layer: int):
+        return (self.num_blocks, self.block_size, self.num_kv_heads, self.head_dims[layer])
+
+    def get_key_cache(self, layer: int) -> np.ndarray:
+        """Host copy of layer's K pages ([numBlocks, blockSize, Hkv, d])."""
+        return self.read(layer, 0)
+
+    def get_value_cache(self, layer: int) -> np.ndarray:
+        return self.read(layer, 1)
+
+    def read(self, layer: int, which: int, offset: int = 0, count: int = None) -> np.ndarray:
+        _, _, nbytes = self._layer(layer)
+        total = nbytes // 4
+        count = total - offset if count is None else count
+        out = np.empty(count, np.float32)
+        _check(self._ctx.handle, N.load().nva_kv_read(self._h, layer, which, offset, _ptr(out),
+                                                      count), "KvCacheArena read")
+        if offset == 0 and count == total:
+            return out.reshape(self.shape(layer))
+        return out
+
+    def write(self, layer: int, which: int, data: np.ndarray, offset: int = 0) -> None:
+        data = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        _check(self._ctx.handle, N.load().nva_kv_write(self._h, layer, which, offset,
+                                                       _ptr(data), data.size),
+               "KvCacheArena write")
+
+    def device_ptrs(self, layer: int):
+        k, v, n = self._layer(layer)
+        return k, v, n
+
+    def close(self) -> None:
+        if self._h:
+            N.load().nva_kv_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class RotaryEmbedding:
+    """RotaryEmbedding(headSize, rotaryDim, maxPositionEmbeddings, base) (Norms.java:171-205).
+
+    ``cos_sin`` may pass the caller's own [maxPos, headSize] table (the Java table); otherwise
+    the library builds it with the reference's arithmetic."""
+
+    def __init__(self, ctx: Context, head_size: int, rotary_dim: int, max_position_embeddings: int,
+                 base: float, cos_sin: Optional[np.ndarray] = None):
+        lib = N.load()
+        h = ctypes.c_void_p()
+        if cos_sin is not None:
+            t = np.ascontiguousarray(cos_sin, dtype=np.float32)
+            if t.shape != (max_position_embeddings, head_size):
+                raise IllegalArgumentException("cos_sin must be [maxPos, headSize]")
+            st = lib.nva_rope_create(ctx.handle, _ptr(t), max_position_embeddings, head_size,
+                                     ctypes.byref(h))
+        else:
+            st = lib.nva_rope_create_theta(ctx.handle, head_size, rotary_dim,
+                                           max_position_embeddings,
+                                           float(np.float32(base)), ctypes.byref(h))
+        _check(ctx.handle, st, "RotaryEmbedding")
+        self._h = h
+        self.head_size = head_size
+        self.max_position = max_position_embeddings
+
+    @property
+    def handle(self):
+        return self._h
+
+    def forward(self, positions, query: torch.Tensor, key: torch.Tensor, ctx: Context):
+        """RotaryEmbedding.forward(positions, query, key, context) -> (q_rot, k_rot)."""
+        if positions is not None:
+            ctx.set_positions(positions)
+        if query.dim() != 3 or key.dim() != 3:
+            raise IllegalArgumentException("query and key must be [tokens, heads, headSize]")
+        tokens, hq, d = query.shape
+        hk = key.shape[1]
+        if d != self.head_size or key.shape[2] != d or key.shape[0] != tokens:
+            raise IllegalArgumentException("query/key shapes do not match the RoPE head size")
+        q_out = torch.empty_like(query)
+        k_out = torch.empty_like(key)
+        _check(ctx.handle, N.load().nva_rope_forward(
+            ctx.handle, self._h, _dev(query, "query"), _dev(key, "key"), tokens, hq, hk,
+            _dev(q_out, "q_out"), _dev(k_out, "k_out")), "RotaryEmbedding.forward")
+        return q_out, k_out
+
+    def close(self) -> None:
+        if self._h:
+            N.load().nva_rope_destroy(self._h)
+            self._h = None
+
+
+class Attention:
+    """Attention(numHeads, headDim, scale, numKvHeads, slidingWindow, kvLayerIndex, writeKv)
+    (Attention.java:70-125)."""
+
+    def __init__(self, num_heads: int, head_dim: int, scale: float, num_kv_heads: int,
+                 sliding_window: int = 0, kv_layer_index: int = 0, write_kv: bool = True):
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = float(np.float32(scale))
+        self.num_kv_heads = num_kv_heads
+        self.sliding_window = max(0, int(sliding_window))
+        self.kv_layer_index = kv_layer_index
+        self.write_kv = bool(write_kv)
+        self._desc = N.AttnDesc(num_heads, head_dim, self.scale, num_kv_heads,
+                                self.sliding_window, kv_layer_index, int(self.write_kv))
+
+    def _check_shapes(self, q, k, v) -> None:
+        if q.dim() != 3 or tuple(q.shape[1:]) != (self.num_heads, self.head_dim):
+            raise IllegalArgumentException(
+                f"q must be [tokens, {self.num_heads}, {self.head_dim}], got {tuple(q.shape)}")
+        for name, t in (("k", k), ("v", v)):
+            if t is not None and tuple(t.shape) != (q.shape[0], self.num_kv_heads, self.head_dim):
+                raise IllegalArgumentException(
+                    f"{name} must be [{q.shape[0]}, {self.num_kv_heads}, {self.head_dim}], "
+                    f"got {tuple(t.shape)}")
+
+    def forward(self, q: torch.Tensor, k: Optional[torch.Tensor], v: Optional[torch.Tensor],
+                ctx: Context) -> torch.Tensor:
+        """Attention.forward(q, k, v, ctx) (Attention.java:152-171): stores k/v into the bound
+        arena at the step's slots, then attends; returns a new [tokens, numHeads, headDim]."""
+        self._check_shapes(q, k, v)
+        arena = ctx.kv_cache()
+        out = torch.empty((q.shape[0], self.num_heads, self.head_dim), dtype=torch.float32,
+                          device=q.device)
+        _check(ctx.handle, N.load().nva_attention_forward(
+            ctx.handle, arena.handle if arena is not None else None, ctypes.byref(self._desc),
+            _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), q.shape[0], _dev(out, "out")),
+            "Attention.forward")
+        return out
+
+    def forward_with_rope(self, rope: RotaryEmbedding, positions, q: torch.Tensor,
+                          k: torch.Tensor, v: torch.Tensor, ctx: Context,
+                          q_out: Optional[torch.Tensor] = None,
+                          k_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """RotaryEmbedding.forward + Attention.forward in one call (the fused RoPE + store
+        kernel, then attention), as Qwen3Attention.forward uses them
+        (models/internal/Qwen3ForCausalLM.java:207-222)."""
+        self._check_shapes(q, k, v)
+        for t, shape in ((q_out, q.shape), (k_out, k.shape)):
+            if t is not None and tuple(t.shape) != tuple(shape):
+                raise IllegalArgumentException("q_out/k_out must match q/k")
+        if positions is not None:
+            ctx.set_positions(positions)
+        arena = ctx.kv_cache()
+        out = torch.empty((q.shape[0], self.num_heads, self.head_dim), dtype=torch.float32,
+                          device=q.device)
+        _check(ctx.handle, N.load().nva_rope_attention_forward(
+            ctx.handle, arena.handle if arena is not None else None, rope.handle,
+            ctypes.byref(self._desc), _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), q.shape[0],
+            _dev(q_out, "q_out"), _dev(k_out, "k_out"), _dev(out, "out")),
+            "Attention.forward_with_rope")
+        return out
