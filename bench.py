@@ -1,0 +1,305 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged attention path on one MI355X.
+
+One step = one attention layer pass over one scheduler step's batch, with the step metadata
+already uploaded and every input resident in HBM: the fused RoPE + K/V store kernel, then the
+attention kernels (split-KV decode + merge, or MFMA prefill).
+
+Headline (``value``): decode attention at the Qwen3-0.6B shape with 256 sequences of
+log-uniform context in [128, 32768] (fragmented block tables, ~15 GB of K/V resident), in GB/s
+of algorithmic bytes (each KV head's K and V rows read once, plus q/out/tables).  Reported
+beside it: varlen causal prefill at the Qwen3-0.6B shape (512/1024/1536/2048, second half of
+the last sequence served from 4 cached pages) in TFLOP/s of unmasked (q,k) pairs
+(4 * head_dim * q_heads per pair).  Both carry a roofline object for their dominant kernel,
+timed with HIP events on the library's stream during the timed region.
+
+The CPU baseline is the oracle (a C restatement of the reference's Attention.attendJobs with its
+head-major parallel split), timed on the host on a bounded sample of the same decode workload.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "nano-vllm-java_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode-attn HBM GB/s (% of peak) + prefill-attn TFLOP/s, Qwen3-0.6B shape"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU work budget of the baseline")
+    ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def torch_view(ptr, count, device):
+    """A float32 torch tensor over device memory the library owns."""
+    import torch
+
+    class _Cai:
+        pass
+
+    obj = _Cai()
+    obj.__cuda_array_interface__ = {"shape": (count,), "typestr": "<f4",
+                                    "data": (ptr, False), "version": 2, "strides": None}
+    return torch.as_tensor(obj, device=f"cuda:{device}")
+
+
+def fill_arena_normal(arena, layer, seed):
+    import torch
+    k_ptr, v_ptr, nbytes = arena.device_ptrs(layer)
+    n = nbytes // 4
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    for ptr in (k_ptr, v_ptr):
+        t = torch_view(ptr, n, 0)
+        chunk = 1 << 28
+        for s in range(0, n, chunk):
+            t[s:s + chunk].normal_(generator=g)
+    torch.cuda.synchronize()
+
+
+def decode_bytes(wl):
+    """Algorithmic bytes of one decode step: K+V rows (per KV head, window-limited), q in,
+    out written, block-table entries and context lengths read."""
+    kv = wl.kv_bytes_read()
+    rows = len(wl.seqs)
+    qo = rows * wl.hq * wl.d * 4 * 2
+    pages = sum(-(-(c + n) // wl.block_size) for c, n in wl.seqs)
+    return kv + qo + 4 * (pages + rows)
+
+
+def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, label):
+    import torch
+    from nanollvm_amd import Context  # noqa: F401
+
+    ctx.set(**wl.meta.context_args())
+    ctx.bind_kv_cache(arena)
+    pos = wl.meta.positions
+    for _ in range(warmup):
+        attn.forward_with_rope(rope, pos, q, k, v, ctx, q_out=out_q, k_out=out_k)
+    torch.cuda.synchronize()
+    ctx.reset_stats()
+    ctx.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        attn.forward_with_rope(rope, pos, q, k, v, ctx, q_out=out_q, k_out=out_k)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ctx.set_timing(False)
+    stats = {name: ctx.kernel_stats(name) for name in ("rope_store", "decode", "merge",
+                                                       "prefill")}
+    ms = (t1 - t0) * 1e3 / steps
+    log(f"{label}: {ms:.4f} ms/step; kernels " + ", ".join(
+        f"{n}={s[1] / max(s[0], 1):.4f}ms x{s[0]}" for n, s in stats.items() if s[0]))
+    return ms, stats
+
+
+def bench_decode(args, ctx):
+    import torch
+    from nanollvm_amd import Attention, KvCacheArena, RotaryEmbedding
+    from nanollvm_amd import workloads as W
+
+    wl = W.qwen3_decode_large()
+    log(f"decode workload: {wl.name}: {len(wl.seqs)} rows, {sum(c + n for c, n in wl.seqs)} "
+        f"tokens, {wl.num_blocks} blocks")
+    arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+    fill_arena_normal(arena, 0, 1234)
+    rope = RotaryEmbedding(ctx, wl.d, wl.d, wl.max_pos, wl.rope_theta)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    T = wl.tokens
+    q = torch.randn((T, wl.hq, wl.d), device="cuda", generator=g)
+    k = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
+    v = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
+    oq = torch.empty_like(q)
+    ok = torch.empty_like(k)
+    attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
+    ms, stats = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, ok, args.steps, args.warmup,
+                          "decode")
+    byts = decode_bytes(wl)
+    n_dec, t_dec = stats["decode"]
+    dec_ms = t_dec / max(n_dec, 1)
+    achieved = byts / (dec_ms * 1e-3) / 1e9
+    res = {
+        "wl": wl, "ms": ms, "bytes": byts, "gbs": byts / (ms * 1e-3) / 1e9,
+        "kernel_ms": {n: s[1] / max(s[0], 1) for n, s in stats.items() if s[0]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "row_attention_kernel<128,2> (split-KV decode)",
+                     "algorithmic_bytes_per_launch": byts},
+    }
+    rope.close()
+    arena.close()
+    return res
+
+
+def bench_prefill(args, ctx):
+    import torch
+    from nanollvm_amd import Attention, KvCacheArena, RotaryEmbedding
+    from nanollvm_amd import workloads as W
+
+    wl = W.qwen3_prefill()
+    arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+    fill_arena_normal(arena, 0, 99)
+    rope = RotaryEmbedding(ctx, wl.d, wl.d, wl.max_pos, wl.rope_theta)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    T = wl.tokens
+    q = torch.randn((T, wl.hq, wl.d), device="cuda", generator=g)
+    k = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
+    v = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
+    oq = torch.empty_like(q)
+    ok = torch.empty_like(k)
+    attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
+    ms, stats = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, ok, args.steps, args.warmup,
+                          "prefill")
+    flops = 4.0 * wl.d * wl.hq * wl.visible_pairs()
+    n_pf, t_pf = stats["prefill"]
+    pf_ms = t_pf / max(n_pf, 1)
+    achieved = flops / (pf_ms * 1e-3) / 1e12
+    res = {
+        "workload": wl.name, "ms_per_step": round(ms, 5),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "kernel_ms": {n: round(s[1] / max(s[0], 1), 5) for n, s in stats.items() if s[0]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "prefill_kernel<128,2> (fp32 MFMA 32x32x2)",
+                     "algorithmic_flops_per_launch": flops},
+    }
+    rope.close()
+    arena.close()
+    return res
+
+
+def cpu_baseline(wl, budget_s):
+    """Times the oracle's Attention.forward (decode branch) on the host on the first rows of the
+    decode workload (at most 1024 pages of K/V), repeating it for about budget_s seconds."""
+    import numpy as np
+    from oracle import oracle as O
+    from nanollvm_amd import workloads as W
+
+    threads = min(16, os.cpu_count() or 1)
+    rows, pages = 0, 0
+    for c, n in wl.seqs:
+        p = -(-(c + n) // wl.block_size)
+        if rows and pages + p > 1024:
+            break
+        rows, pages = rows + 1, pages + p
+    seqs = wl.seqs[:rows]
+    sub = W.build("cpu sample", seqs, is_prefill=False, hq=wl.hq, hkv=wl.hkv, d=wl.d,
+                  scale=wl.scale, rng=np.random.default_rng(0))
+    m = sub.meta
+    rng = np.random.default_rng(5)
+    shape = (sub.num_blocks, sub.block_size, sub.hkv, sub.d)
+    block = rng.standard_normal(1 << 20, dtype=np.float32)
+    n = int(np.prod(shape))
+    kc = np.resize(block, n).reshape(shape)
+    vc = np.resize(block[::-1].copy(), n).reshape(shape)
+    q = rng.standard_normal((rows, sub.hq, sub.d), dtype=np.float32)
+    kv = rng.standard_normal((rows, sub.hkv, sub.d), dtype=np.float32)
+
+    def once(nthreads):
+        t0 = time.perf_counter()
+        O.attention_forward(sub.hq, sub.d, sub.scale, sub.hkv, is_prefill=False, q=q, k=kv,
+                            v=kv, slot_mapping=m.slot_mapping, context_lens=m.context_lens,
+                            block_tables=m.block_tables, k_cache=kc, v_cache=vc,
+                            threads=nthreads)
+        return time.perf_counter() - t0
+
+    byts = decode_bytes(sub)
+    toks = int(sum(c + n for c, n in seqs))
+    dt1 = once(1)
+    reps, spent = 0, 0.0
+    while reps == 0 or spent < max(0.0, budget_s - dt1):
+        spent += once(threads)
+        reps += 1
+    dt = spent / reps
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(byts / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"decode rows 0..{rows - 1} of the same workload ({toks} context tokens, "
+                      f"{pages} pages, {byts / 1e9:.2f} GB algorithmic per pass), oracle (C "
+                      f"restatement of Attention.attendJobs, scalar-kernel semantics), "
+                      f"{threads} threads with the reference's head-major split, mean of "
+                      f"{reps} passes of {dt:.3f} s",
+            "single_thread_gbs": round(byts / dt1 / 1e9, 3), "cpu_model": cpu_model}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus above 1 is not "
+                                   "supported (the path shards by sequence or KV head with no "
+                                   "exchange, but only the one-GPU kernel is built)"}))
+        sys.exit(2)
+    import torch
+    from nanollvm_amd import Context
+
+    torch.cuda.init()
+    ctx = Context(0)
+    dec = pf = None
+    if args.only in (None, "decode"):
+        dec = bench_decode(args, ctx)
+    if args.only in (None, "prefill"):
+        pf = bench_prefill(args, ctx)
+    ctx.close()
+    cpu = None
+    if dec is not None and not args.no_cpu:
+        cpu = cpu_baseline(dec["wl"], args.cpu_seconds)
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded N(0,1) q/k/v and pages; seeded block tables)"}
+    if dec is not None:
+        wl = dec["wl"]
+        line.update({
+            "value": round(dec["gbs"], 1), "unit": "GB/s", "ms_per_step": round(dec["ms"], 5),
+            "config": {"workload": wl.name, "q_heads": wl.hq, "kv_heads": wl.hkv,
+                       "head_dim": wl.d, "block_size": wl.block_size, "rows": len(wl.seqs),
+                       "context_tokens": int(sum(c + n for c, n in wl.seqs)),
+                       "kv_bytes_per_step": wl.kv_bytes_read(),
+                       "step": "fused RoPE+store, split-KV decode, merge"},
+            "tokens_per_s_per_layer": round(len(wl.seqs) / (dec["ms"] * 1e-3), 1),
+            "kernel_ms": {n: round(x, 5) for n, x in dec["kernel_ms"].items()},
+            "roofline": dec["roofline"],
+        })
+    else:
+        line.update({"value": pf["tflops"], "unit": "TFLOP/s", "ms_per_step": pf["ms_per_step"],
+                     "config": {"workload": pf["workload"]}, "roofline": pf["roofline"]})
+    if pf is not None:
+        line["prefill"] = pf
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
