@@ -364,6 +364,10 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
           ti.kbase = kbase;
           ti.ks = W > 0 ? std::max(0, aq0 - W + 1) : 0;
           ti.ke = aq1 + 1;
+          ti.part = -1;
+          ti.nsplit = 1;
+          ti.split = 0;
+          ti.pad = 0;
           tiles.push_back(ti);
         }
       } else {
@@ -377,6 +381,52 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     }
   }
   plan->covers_all = covered == key.tokens;
+
+  // Split the key range of long prefill tiles so that no workgroup's serial chain of key tiles
+  // is much longer than the average share of a workgroup slot (two per CU).  The chunks of a
+  // tile write partials (query-major, chunk-minor) that the merge kernel combines.
+  std::vector<MergeItem> merges;
+  int parts = 0;
+  if (!tiles.empty()) {
+    int64_t keys = 0;
+    for (const TileItem &t : tiles) keys += t.ke - t.ks;
+    const int64_t slots = (int64_t)ctx->num_cus * 2;
+    const int64_t share = (keys * key.wg_per_item + slots - 1) / slots;
+    int target = (int)std::max<int64_t>(256, ((share + 31) / 32) * 32);
+    if (paged) {
+      // A chunk's pages must fit the kernel's LDS copy of the block table.
+      const int64_t cap = (int64_t)(kPrefillTablePages - 2) * key.block_size / 32 * 32;
+      target = (int)std::max<int64_t>(32, std::min<int64_t>(target, cap));
+    }
+    std::vector<TileItem> split;
+    split.reserve(tiles.size() * 2);
+    for (const TileItem &t : tiles) {
+      const int len = t.ke - t.ks;
+      const bool fits = !paged || (t.ke - 1) / key.block_size - t.ks / key.block_size + 1 <=
+                                      kPrefillTablePages;
+      if (fits && len <= target + target / 4) {
+        split.push_back(t);
+        continue;
+      }
+      const int n = (len + target - 1) / target;
+      const int step = ((len + n - 1) / n + 31) / 32 * 32;
+      const int rows = std::min(key.tile_q, t.qlen - t.q0);
+      int made = 0;
+      for (int k0 = t.ks; k0 < t.ke; k0 += step) made++;
+      for (int j = 0; j < made; j++) {
+        TileItem c = t;
+        c.ks = t.ks + j * step;
+        c.ke = std::min(t.ke, c.ks + step);
+        c.part = parts;
+        c.nsplit = made;
+        c.split = j;
+        split.push_back(c);
+      }
+      for (int r = 0; r < rows; r++) merges.push_back({t.qstart + t.q0 + r, parts + r * made, made, 0});
+      parts += rows * made;
+    }
+    tiles.swap(split);
+  }
   // Longest tiles first: the grid is dispatched roughly in order, so this is an LPT schedule.
   std::stable_sort(tiles.begin(), tiles.end(), [](const TileItem &a, const TileItem &b) {
     return (a.ke - a.ks) > (b.ke - b.ks);
@@ -400,9 +450,7 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   }
 
   std::vector<RowItem> items;
-  std::vector<MergeItem> merges;
   items.reserve(rows.size() + total / chunk + 1);
-  int parts = 0;
   for (const Row &r : rows) {
     const int len = r.kend - r.kbeg;
     if (len <= 0) {
@@ -501,6 +549,12 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
             "zero output");
   }
   char *pbase = static_cast<char *>(plan->dev.ptr);
+  const size_t parts = (size_t)plan->num_parts * d.num_heads;
+  if (parts > 0) {
+    const size_t need = parts * (2 + (size_t)d.head_dim) * sizeof(float);
+    HIP_TRY(ctx, ctx->d_part.reserve(need), "partial buffer");
+  }
+  float *pm = static_cast<float *>(ctx->d_part.ptr);
   if (plan->num_tiles > 0) {
     TileLaunch t;
     t.q = q;
@@ -513,15 +567,14 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     t.head_dim = d.head_dim;
     t.window = key.window;
     t.scale = d.scale;
+    t.part_m = pm;
+    t.part_l = pm + parts;
+    t.part_acc = pm + 2 * parts;
     Timed tm(ctx, "prefill");
     HIP_TRY(ctx, launch_prefill_tiles(t, hpw_tile, ctx->stream), "prefill kernel launch");
     tm.done();
   }
   if (plan->num_rows > 0) {
-    const size_t parts = (size_t)plan->num_parts * d.num_heads;
-    const size_t need = parts * (2 + (size_t)d.head_dim) * sizeof(float);
-    HIP_TRY(ctx, ctx->d_part.reserve(need), "partial buffer");
-    float *pm = static_cast<float *>(ctx->d_part.ptr);
     RowLaunch r;
     r.q = q;
     r.out = out;
@@ -540,8 +593,6 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     tm.done();
   }
   if (plan->num_merge > 0) {
-    const size_t parts = (size_t)plan->num_parts * d.num_heads;
-    float *pm = static_cast<float *>(ctx->d_part.ptr);
     MergeLaunch mg;
     mg.out = out;
     mg.items = reinterpret_cast<const MergeItem *>(pbase + plan->off_merge);

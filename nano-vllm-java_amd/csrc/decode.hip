@@ -6,8 +6,9 @@
 // (slot(t) = table[t / BS] * BS + t % BS, Attention.java:131-137) with the KV head
 // kvh = h / rep, score = dot(q, k) * scale, softmax over the keys, out = sum(w v) / sum(w),
 // and out = 0 when no key is visible.  The reference's 64-key online softmax is replaced by a
-// per-stream online softmax over 8-key groups and a final log-sum-exp merge of the streams;
-// the result agrees to fp32 rounding.
+// per-stream online softmax over 8-key groups and a final log-sum-exp merge of the streams, in
+// the log2 domain (scores scaled by scale * log2 e, v_exp_f32); the result agrees with the
+// reference to fp32 rounding.
 //
 // Mapping onto CDNA4 (wave64):
 //   * one workgroup (4 waves) per (work item, KV head, group of HPW query heads); a work item
@@ -92,6 +93,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   float4 qv[HPW];
 #pragma unroll
   for (int h = 0; h < HPW; h++) qv[h] = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + c * 4);
+  const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
 
   const size_t rs = (size_t)a.hkv * D;
   const float *kp = a.kv.k + (size_t)kvh * D + c * 4;
@@ -132,17 +134,17 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       float mx = -INFINITY;
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        s[u] = ok[u] ? s[u] * a.scale : -INFINITY;
+        s[u] = ok[u] ? s[u] * sl2 : -INFINITY;
         mx = fmaxf(mx, s[u]);
       }
       const float mn = fmaxf(m[h], mx);
       const float ms = mn == -INFINITY ? 0.0f : mn;
-      const float alpha = expf(m[h] - ms);
+      const float alpha = __builtin_amdgcn_exp2f(m[h] - ms);
       float ls = 0.0f;
       float4 av = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        const float w = expf(s[u] - ms);
+        const float w = __builtin_amdgcn_exp2f(s[u] - ms);
         ls += w;
         av.x = fmaf(w, vr[u].x, av.x);
         av.y = fmaf(w, vr[u].y, av.y);
@@ -178,7 +180,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     float L = 0.0f;
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s = 0; s < NS; s++) {
-      const float e = expf(sm_m[s][h] - Ms);
+      const float e = __builtin_amdgcn_exp2f(sm_m[s][h] - Ms);
       L = fmaf(sm_l[s][h], e, L);
       const float4 x = sm_acc[s][h][cc];
       A.x = fmaf(x.x, e, A.x);
@@ -217,7 +219,7 @@ __global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
       float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
       for (int p = 0; p < it.nparts; p++) {
         const size_t pi = (size_t)(it.first + p) * a.hq + h;
-        const float e = expf(a.part_m[pi] - Ms);
+        const float e = __builtin_amdgcn_exp2f(a.part_m[pi] - Ms);
         L = fmaf(a.part_l[pi], e, L);
         const float4 x = ld4(a.part_acc + pi * a.head_dim + cc * 4);
         A.x = fmaf(x.x, e, A.x);

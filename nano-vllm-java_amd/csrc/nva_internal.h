@@ -21,7 +21,8 @@ struct RowItem {
 };
 
 // Combines the partials of one split row (nparts >= 2) or zero-fills a row with no visible
-// key (nparts == 0), as Attention.java:393-394 gives 0 when l == 0.
+// key (nparts == 0), as Attention.java:393-394 gives 0 when l == 0.  Partial maxima are in
+// log2 units (scores are scaled by scale * log2(e) in every kernel).
 struct MergeItem {
   int32_t qrow;
   int32_t first;
@@ -38,8 +39,12 @@ struct TileItem {
   int32_t q0;      // first query of this tile (index within the sequence)
   int32_t klen;    // keys of the sequence (kLen in the reference)
   int32_t kbase;   // dense K/V: row of key 0; paged: unused
-  int32_t ks;      // first key any query of the tile sees
-  int32_t ke;      // one past the last key any query of the tile sees
+  int32_t ks;      // first key of this workgroup's key chunk
+  int32_t ke;      // one past the last key of the chunk
+  int32_t part;    // partial-result base of a split tile, or -1 (whole key range: write out)
+  int32_t nsplit;  // key chunks the tile is split into
+  int32_t split;   // this chunk's index
+  int32_t pad;
 };
 
 struct KvView {
@@ -80,6 +85,7 @@ struct TileLaunch {
   int32_t hq, hkv, head_dim;
   int32_t window;  // 0 = none
   float scale;
+  float *part_m, *part_l, *part_acc;  // split tiles: [P, Hq], [P, Hq], [P, Hq, D]
 };
 
 struct RopeStoreLaunch {
@@ -109,6 +115,9 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream
 // Shapes the kernels are instantiated for.
 bool row_kernel_supports(int head_dim, int heads_per_wg);
 bool prefill_kernel_supports(int head_dim, int heads_per_wg);
+
+// Most pages one prefill key chunk may span (its block ids are staged in LDS).
+constexpr int kPrefillTablePages = 128;
 
 // Query rows per prefill workgroup for a given heads-per-workgroup choice.
 inline int prefill_tile_queries(int heads_per_wg) { return 32 * (4 / heads_per_wg); }

@@ -7,18 +7,27 @@
 // Keys come from dense k/v rows (prefillDense) or from the cache through the block table
 // (prefillWithCache).
 //
-// Mapping onto CDNA4: a workgroup (4 waves) owns a tile of queries of one sequence for one
-// KV head and HPW of its query heads; wave w handles 32 queries of one head.  Key tiles of 32
-// rows of K and V are staged in LDS (coalesced 512-byte row loads, prefetched into registers
-// one tile ahead) and shared by the 4 waves.  Per key tile each wave computes
-//   S^T[key][query] = K Q^T      64 x v_mfma_f32_32x32x2_f32 (D = 128)
-//   O^T[dim][query] += V^T P^T   64 x v_mfma_f32_32x32x2_f32
-// With S transposed, each lane holds 16 keys of ONE query, so the softmax row max is an
-// in-lane max plus one exchange with lane^32, and the running sum needs no exchange until the
-// end.  The P^T values land in exactly the registers the PV MFMA reads as its B operand (the
-// contraction order over keys is permuted to match), so P never goes through LDS.  Only tiles
-// that cross the causal diagonal, the window edge or the end of the keys are masked; all
-// others run unmasked.  Q (32 x D/2 per lane) stays in registers for the whole key loop.
+// Mapping onto CDNA4.  A workgroup (4 waves) owns a tile of queries of one sequence for one KV
+// head and HPW of its query heads, over one chunk [ks, ke) of the keys (long key ranges are
+// split across workgroups and merged afterwards, so no workgroup's serial chain is much longer
+// than the average).  Wave w handles 32 queries of one head.
+//   * Key tiles of 32 rows of K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
+//     register staging), double-buffered so the next tile streams in while this one is used;
+//     one barrier per tile.  Rows are stored unpadded with their 16-byte chunks XOR-swizzled
+//     by (row & 7), which makes both column reads below conflict-free.
+//   * Per tile each wave computes (D = 128)
+//       S^T[key][query] = K Q^T      64 x v_mfma_f32_32x32x2_f32, K from LDS (ds_read_b128),
+//                                    Q (32 x D/2 per lane) resident in registers;
+//       O^T[dim][query] += V^T P^T   64 x v_mfma_f32_32x32x2_f32, one ds_read_b128 of V feeds
+//                                    4 MFMAs (output block b holds dims 4r + b).
+//     With S transposed each lane holds 16 keys of ONE query: the row max is an in-lane max plus
+//     one exchange with lane^32, and P^T lands exactly in the registers the PV MFMA reads as its
+//     B operand (the key order of the contraction is permuted to match), so P never touches LDS.
+//   * Softmax runs in the log2 domain (scale * log2 e folded into the score, v_exp_f32), and the
+//     running max is only moved -- and O rescaled -- when a tile's max exceeds it by more than
+//     2^8, which after the first tiles almost never happens.
+//   * Only tiles that cross the causal diagonal, the window edge or the end of the keys are
+//     masked.
 #include "nva_internal.h"
 
 namespace nva {
@@ -27,11 +36,25 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyRescale = 8.0f;  // log2 units
+
+}  // namespace
+
+// Pages of one key chunk whose block ids are staged in LDS (the host splits chunks to fit).
+constexpr int kTablePages = kPrefillTablePages;
+
+namespace {
+
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 
-__device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *table, int kbase,
-                                            int t) {
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the block
+// table, which starts at page blk0.
+__device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *stab, int blk0,
+                                            int kbase, int t) {
   if (!kv.paged) return (int64_t)kbase + t;
   int blk, off;
   if (kv.bs_shift >= 0) {
@@ -41,7 +64,7 @@ __device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *tab
     blk = t / kv.block_size;
     off = t - blk * kv.block_size;
   }
-  return (int64_t)table[blk] * kv.block_size + off;
+  return (int64_t)stab[blk - blk0] * kv.block_size + off;
 }
 
 }  // namespace
@@ -49,26 +72,31 @@ __device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *tab
 template <int D, int HPW>
 __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
   constexpr int KT = 32;          // keys per tile
-  constexpr int DP = D + 4;       // padded LDS row (conflict-free b128 column reads)
   constexpr int DH = D / 2;       // QK contraction steps per lane half
-  constexpr int NB = D / 32;      // 32-wide output blocks of O^T
-  constexpr int C4 = D / 4;       // float4 per K/V row
-  constexpr int RPP = 256 / C4;   // rows loaded per pass by the workgroup
-  constexpr int LP = KT / RPP;    // load passes per tile
-  __shared__ __attribute__((aligned(16))) float sk[KT * DP];
-  __shared__ __attribute__((aligned(16))) float sv[KT * DP];
+  constexpr int NB = D / 32;      // output blocks of O^T (block b holds dims NB*r + b)
+  constexpr int C4 = D / 4;       // 16-byte chunks per K/V row
+  constexpr int RPI = 64 / C4;    // rows per wave load instruction
+  constexpr int LPW = KT / RPI / 4;  // load instructions per wave per tensor per tile
+  constexpr int TILE = KT * D;    // floats per K (or V) tile
+  __shared__ __attribute__((aligned(16))) float sk0[TILE];
+  __shared__ __attribute__((aligned(16))) float sv0[TILE];
+  __shared__ __attribute__((aligned(16))) float sk1[TILE];
+  __shared__ __attribute__((aligned(16))) float sv1[TILE];
+  __shared__ int32_t stab[kTablePages];  // block ids of the pages this chunk touches
 
   const TileItem it = a.items[blockIdx.x];
   const int rep = a.hq / a.hkv;
   const int groups = rep / HPW;
   const int kvh = blockIdx.y / groups;
-  const int h = kvh * rep + (blockIdx.y - kvh * groups) * HPW + (threadIdx.x >> 6) % HPW;
-  const int qb = (threadIdx.x >> 6) / HPW;
+  const int wave = threadIdx.x >> 6;
+  const int h = kvh * rep + (blockIdx.y - kvh * groups) * HPW + wave % HPW;
+  const int qb = wave / HPW;
   const int lane = threadIdx.x & 63;
   const int i = lane & 31;
   const int half = lane >> 5;
   const int W = a.window;
   const int off = it.klen - it.qlen;  // absolute position of query 0
+  const float sl2 = a.scale * kLog2e;
 
   // This lane's query (column i of S^T) and its visible key range.
   const int qi = it.q0 + qb * 32 + i;
@@ -77,13 +105,13 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
   const int aq = off + qic;
   const int vis_lo = W > 0 ? max(0, aq - W + 1) : 0;
   const int vis_hi = aq + 1;
-  // The wave's queries: union and intersection of their visible ranges.
+  // The wave's queries: bounds of their visible ranges.
   const int wq0 = it.q0 + qb * 32;
   const bool wave_active = wq0 < it.qlen;
   const int wq1 = min(wq0 + 31, it.qlen - 1);
-  const int wlo_min = W > 0 ? max(0, off + wq0 - W + 1) : 0;  // earliest key any query sees
-  const int wlo_max = W > 0 ? max(0, off + wq1 - W + 1) : 0;  // latest first-visible key
-  const int whi_min = off + wq0 + 1;                            // every query sees < this
+  const int wlo_min = W > 0 ? max(0, off + wq0 - W + 1) : 0;
+  const int wlo_max = W > 0 ? max(0, off + wq1 - W + 1) : 0;
+  const int whi_min = off + wq0 + 1;
   const int whi_max = off + wq1 + 1;
 
   float qr[DH];
@@ -104,67 +132,78 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
   for (int b = 0; b < NB; b++)
 #pragma unroll
     for (int v = 0; v < 16; v++) o[b][v] = 0.0f;
-  float m_run = -INFINITY;
+  float m_run = -INFINITY;  // log2 units
   float l_run = 0.0f;
 
   const size_t rs = (size_t)a.hkv * D;
   const float *kbase = a.kv.k + (size_t)kvh * D;
   const float *vbase = a.kv.v + (size_t)kvh * D;
-  const int32_t *table = a.kv.paged ? a.kv.table + (size_t)it.seq * a.kv.bt_stride : nullptr;
-  const int lrow = threadIdx.x / C4;
-  const int lcol = (threadIdx.x - lrow * C4) * 4;
+  // Stage the chunk's block ids in LDS once, so the tile loads never wait on a global load.
+  int blk0 = 0;
+  if (a.kv.paged) {
+    const int bs = a.kv.block_size;
+    blk0 = it.ks / bs;
+    const int npages = (it.ke - 1) / bs - blk0 + 1;
+    const int32_t *table = a.kv.table + (size_t)it.seq * a.kv.bt_stride + blk0;
+    for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[j];
+    __syncthreads();
+  }
+  // Load geometry: wave instruction g covers rows [g*RPI, g*RPI + RPI); lane -> (row, chunk).
+  const int lrow = lane / C4;
+  const int lpos = lane - lrow * C4;
 
-  float4 pk[LP], pv[LP];
-  auto load_tile = [&](int kt) {
+  auto issue_tile = [&](int kt, float *dk, float *dv) {
 #pragma unroll
-    for (int p = 0; p < LP; p++) {
-      const int key = kt + lrow + p * RPP;
-      if (key < it.klen) {
-        const int64_t row = tile_row(a.kv, table, it.kbase, key);
-        pk[p] = ld4(kbase + row * rs + lcol);
-        pv[p] = ld4(vbase + row * rs + lcol);
-      } else {
-        pk[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-        pv[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+    for (int p = 0; p < LPW; p++) {
+      const int g = p * 4 + wave;
+      const int r = g * RPI + lrow;
+      const int key = min(kt + r, it.ke - 1);  // rows past the chunk are loaded but masked
+      const int64_t row = tile_row(a.kv, stab, blk0, it.kbase, key);
+      const int col = (lpos ^ (r & 7)) * 4;
+      const float *gk = kbase + row * rs + col;
+      const float *gv = vbase + row * rs + col;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)gk,
+          (__attribute__((address_space(3))) void *)(dk + g * RPI * D), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)gv,
+          (__attribute__((address_space(3))) void *)(dv + g * RPI * D), 16, 0, 0);
     }
   };
 
-  load_tile(it.ks);
-  for (int kt = it.ks; kt < it.ke; kt += KT) {
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < LP; p++) {
-      *reinterpret_cast<float4 *>(&sk[(lrow + p * RPP) * DP + lcol]) = pk[p];
-      *reinterpret_cast<float4 *>(&sv[(lrow + p * RPP) * DP + lcol]) = pv[p];
-    }
-    if (kt + KT < it.ke) load_tile(kt + KT);
-    __syncthreads();
-
-    // Skip tiles no query of this wave sees.
-    if (!wave_active || kt >= whi_max || kt + KT <= wlo_min) continue;
+  auto compute_tile = [&](int kt, const float *sk, const float *sv) {
+    if (!wave_active || kt >= whi_max || kt + KT <= wlo_min) return;
     const bool full = (kt + KT <= whi_min) && (kt >= wlo_max);
 
-    // S^T = K Q^T: A[key][k] = K[key][half*DH + s], B[k][query] = Q[query][half*DH + s].
+    // S^T = K Q^T: step s contracts dim half*DH + s; K row i, 16-byte chunk (half*DH+s)/4.
     f32x16 st;
 #pragma unroll
     for (int v = 0; v < 16; v++) st[v] = 0.0f;
-    const float *krow = &sk[i * DP + half * DH];
+    const float *krow = sk + i * D;
 #pragma unroll
     for (int s = 0; s < DH; s += 4) {
-      const float4 kk = *reinterpret_cast<const float4 *>(krow + s);
+      const int c = ((half * DH + s) >> 2) ^ (i & 7);
+      const float4 kk = ld4(krow + c * 4);
       st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qr[s], st, 0, 0, 0);
       st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qr[s + 1], st, 0, 0, 0);
       st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qr[s + 2], st, 0, 0, 0);
       st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qr[s + 3], st, 0, 0, 0);
     }
+    // Keep at most two K reads in flight ahead of the MFMAs (bounds register pressure).
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int s = 0; s < DH / 4 - 2; s++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 
-    // st[v] holds key kt + 8*(v/4) + 4*half + v%4 for query i.
+    // st[v] holds key kt + 8*(v/4) + 4*half + v%4 for query i (log2-scaled below).
     float mx = -INFINITY;
     if (full) {
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        st[v] *= a.scale;
+        st[v] *= sl2;
         mx = fmaxf(mx, st[v]);
       }
     } else {
@@ -172,47 +211,102 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
       for (int v = 0; v < 16; v++) {
         const int key = kt + 8 * (v >> 2) + 4 * half + (v & 3);
         const bool vis = key >= vis_lo && key < vis_hi;
-        st[v] = vis ? st[v] * a.scale : -INFINITY;
+        st[v] = vis ? st[v] * sl2 : -INFINITY;
         mx = fmaxf(mx, st[v]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m_run, mx);
-    const float ms = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = expf(m_run - ms);
-    float ls = 0.0f;
+    mx = fmaxf(mx, xor32(mx));
+    const bool need = mx > m_run + kLazyRescale;
+    if (__any(need)) {
+      const float mn = need ? mx : m_run;
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mn);
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < NB; b++) o[b] *= alpha;
+      m_run = mn;
+    }
+    const float ms = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
-      st[v] = expf(st[v] - ms);
-      ls += st[v];
+      st[v] = __builtin_amdgcn_exp2f(st[v] - ms);
+      l_run += st[v];
     }
-    l_run = fmaf(l_run, alpha, ls);
-    m_run = mn;
-#pragma unroll
-    for (int b = 0; b < NB; b++) o[b] *= alpha;
 
-    // O^T += V^T P^T: step s contracts key 8*(s/4) + 4*half + s%4, which is st[s] in this lane.
+    // O^T += V^T P^T: step s contracts key 8*(s/4) + 4*half + s%4 (= st[s] in this lane); the
+    // A operand of block b is V[key][NB*i + b], read for all blocks at once.
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-#pragma unroll
-      for (int s = 0; s < 16; s++) {
-        const int key = 8 * (s >> 2) + 4 * half + (s & 3);
-        const float vv = sv[key * DP + b * 32 + i];
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, st[s], o[b], 0, 0, 0);
+    for (int s = 0; s < 16; s++) {
+      const int key = 8 * (s >> 2) + 4 * half + (s & 3);
+      const int byte = (i * NB * 4);
+      const int chunk = (byte >> 4) ^ (key & 7);
+      const float *vp = sv + key * D + chunk * 4 + ((byte & 15) >> 2);
+      if constexpr (NB == 4) {
+        const float4 vv = ld4(vp);
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, st[s], o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, st[s], o[1], 0, 0, 0);
+        o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, st[s], o[2], 0, 0, 0);
+        o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, st[s], o[3], 0, 0, 0);
+      } else {
+        const float2 vv = *reinterpret_cast<const float2 *>(vp);
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, st[s], o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, st[s], o[1], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+    for (int s = 0; s < 14; s++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NB, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NB, 1);
+  };
+
+  // Double-buffered key loop with one barrier per tile: at the barrier of tile t every wave
+  // has finished tile t-1 (so its buffer can be refilled with tile t+1) and tile t has landed.
+  const int ntiles = (it.ke - it.ks + KT - 1) / KT;
+  issue_tile(it.ks, sk0, sv0);
+  for (int t = 0; t < ntiles; t += 2) {
+    const int kt = it.ks + t * KT;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile t landed
+    __syncthreads();
+    if (t + 1 < ntiles) issue_tile(kt + KT, sk1, sv1);
+    compute_tile(kt, sk0, sv0);
+    if (t + 1 >= ntiles) break;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 2 < ntiles) issue_tile(kt + 2 * KT, sk0, sv0);
+    compute_tile(kt + KT, sk1, sv1);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot == 0.0f ? 0.0f : 1.0f / l_tot;
-  if (qvalid) {
-    float *op = a.out + ((size_t)(it.qstart + qi) * a.hq + h) * D + 4 * half;
+  const float l_tot = l_run + xor32(l_run);
+  if (!qvalid || !wave_active) return;
+  if (it.part < 0) {
+    const float inv = l_tot == 0.0f ? 0.0f : 1.0f / l_tot;
+    float *op = a.out + ((size_t)(it.qstart + qi) * a.hq + h) * D;
 #pragma unroll
-    for (int b = 0; b < NB; b++)
+    for (int v = 0; v < 16; v++) {
+      const int r = 8 * (v >> 2) + 4 * half + (v & 3);
+      if constexpr (NB == 4)
+        st4(op + 4 * r, make_float4(o[0][v] * inv, o[1][v] * inv, o[2][v] * inv, o[3][v] * inv));
+      else
+        *reinterpret_cast<float2 *>(op + 2 * r) = make_float2(o[0][v] * inv, o[1][v] * inv);
+    }
+  } else {
+    // Partial of one key chunk: rows of the tile are laid out query-major, chunk-minor.
+    const size_t p = ((size_t)it.part + (size_t)(qi - it.q0) * it.nsplit + it.split) * a.hq + h;
+    float *op = a.part_acc + p * D;
 #pragma unroll
-      for (int g = 0; g < 4; g++)
-        st4(op + b * 32 + 8 * g, make_float4(o[b][4 * g] * inv, o[b][4 * g + 1] * inv,
-                                             o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv));
+    for (int v = 0; v < 16; v++) {
+      const int r = 8 * (v >> 2) + 4 * half + (v & 3);
+      if constexpr (NB == 4)
+        st4(op + 4 * r, make_float4(o[0][v], o[1][v], o[2][v], o[3][v]));
+      else
+        *reinterpret_cast<float2 *>(op + 2 * r) = make_float2(o[0][v], o[1][v]);
+    }
+    if (half == 0) {
+      a.part_m[p] = m_run;
+      a.part_l[p] = l_tot;
+    }
   }
 }
 
