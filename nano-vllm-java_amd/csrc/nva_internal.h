@@ -120,6 +120,6 @@ bool prefill_kernel_supports(int head_dim, int heads_per_wg);
 constexpr int kPrefillTablePages = 128;
 
 // Query rows per prefill workgroup for a given heads-per-workgroup choice.
-inline int prefill_tile_queries(int heads_per_wg) { return 32 * (4 / heads_per_wg); }
+inline int prefill_tile_queries(int heads_per_wg) { return 16 * (8 / heads_per_wg); }
 
 }  // namespace nva

@@ -13,8 +13,9 @@
 // than the average).  Wave w handles 32 queries of one head.
 //   * Key tiles of 32 rows of K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
 //     register staging), double-buffered so the next tile streams in while this one is used;
-//     one barrier per tile.  Rows are stored unpadded with their 16-byte chunks XOR-swizzled
-//     by (row & 7), which makes both column reads below conflict-free.
+//     one barrier per tile.  Rows are stored unpadded; K rows have their 16-byte chunks
+//     XOR-swizzled by (row & 7) so the column reads of QK are conflict-free, V rows are read
+//     along the row and need no swizzle.
 //   * Per tile each wave computes (D = 128)
 //       S^T[key][query] = K Q^T      64 x v_mfma_f32_32x32x2_f32, K from LDS (ds_read_b128),
 //                                    Q (32 x D/2 per lane) resident in registers;
@@ -32,7 +33,7 @@
 
 namespace nva {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -48,8 +49,6 @@ namespace {
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
-
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
 
 // Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the block
 // table, which starts at page blk0.
@@ -70,14 +69,17 @@ __device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *sta
 }  // namespace
 
 template <int D, int HPW>
-__global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
-  constexpr int KT = 32;          // keys per tile
-  constexpr int DH = D / 2;       // QK contraction steps per lane half
-  constexpr int NB = D / 32;      // output blocks of O^T (block b holds dims NB*r + b)
-  constexpr int C4 = D / 4;       // 16-byte chunks per K/V row
-  constexpr int RPI = 64 / C4;    // rows per wave load instruction
-  constexpr int LPW = KT / RPI / 4;  // load instructions per wave per tensor per tile
-  constexpr int TILE = KT * D;    // floats per K (or V) tile
+__global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
+  constexpr int NW = 8;            // waves per workgroup
+  constexpr int KT = 32;           // keys per tile (two 16-key MFMA blocks)
+  constexpr int DQ = D / 4;        // QK contraction steps per lane group g: dims [DQ*g, DQ*g+DQ)
+  constexpr int NB = D / 16;       // O^T blocks of 16 dims: block 4*hh+bb holds dims 64*hh+4r+bb
+  constexpr int H64 = D / 64;      // 64-dim halves of a V row (one ds_read_b128 each)
+  constexpr int C4 = D / 4;        // 16-byte chunks per K/V row
+  constexpr int RPI = 64 / C4;     // rows per wave load instruction
+  constexpr int LPW = KT / RPI / NW;  // load instructions per wave per tensor per tile
+  constexpr int TILE = KT * D;     // floats per K (or V) tile
+  static_assert(LPW >= 1, "tile too small for the workgroup");
   __shared__ __attribute__((aligned(16))) float sk0[TILE];
   __shared__ __attribute__((aligned(16))) float sv0[TILE];
   __shared__ __attribute__((aligned(16))) float sk1[TILE];
@@ -92,33 +94,34 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
   const int h = kvh * rep + (blockIdx.y - kvh * groups) * HPW + wave % HPW;
   const int qb = wave / HPW;
   const int lane = threadIdx.x & 63;
-  const int i = lane & 31;
-  const int half = lane >> 5;
+  const int i = lane & 15;   // MFMA row/column index of this lane
+  const int g = lane >> 4;   // MFMA k-slot (lane group)
   const int W = a.window;
   const int off = it.klen - it.qlen;  // absolute position of query 0
   const float sl2 = a.scale * kLog2e;
 
   // This lane's query (column i of S^T) and its visible key range.
-  const int qi = it.q0 + qb * 32 + i;
+  const int qi = it.q0 + qb * 16 + i;
   const bool qvalid = qi < it.qlen;
   const int qic = qvalid ? qi : it.qlen - 1;
   const int aq = off + qic;
   const int vis_lo = W > 0 ? max(0, aq - W + 1) : 0;
   const int vis_hi = aq + 1;
-  // The wave's queries: bounds of their visible ranges.
-  const int wq0 = it.q0 + qb * 32;
+  // The wave's 16 queries: bounds of their visible ranges.
+  const int wq0 = it.q0 + qb * 16;
   const bool wave_active = wq0 < it.qlen;
-  const int wq1 = min(wq0 + 31, it.qlen - 1);
+  const int wq1 = min(wq0 + 15, it.qlen - 1);
   const int wlo_min = W > 0 ? max(0, off + wq0 - W + 1) : 0;
   const int wlo_max = W > 0 ? max(0, off + wq1 - W + 1) : 0;
   const int whi_min = off + wq0 + 1;
   const int whi_max = off + wq1 + 1;
 
-  float qr[DH];
+  // Q^T operand: lane (i, g) holds Q[query i][DQ*g + s], s < DQ, for the whole key loop.
+  float qr[DQ];
   {
-    const float *qp = a.q + ((size_t)(it.qstart + qic) * a.hq + h) * D + half * DH;
+    const float *qp = a.q + ((size_t)(it.qstart + qic) * a.hq + h) * D + DQ * g;
 #pragma unroll
-    for (int s = 0; s < DH; s += 4) {
+    for (int s = 0; s < DQ; s += 4) {
       const float4 x = ld4(qp + s);
       qr[s] = x.x;
       qr[s + 1] = x.y;
@@ -127,11 +130,9 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
     }
   }
 
-  f32x16 o[NB];
+  f32x4 o[NB];
 #pragma unroll
-  for (int b = 0; b < NB; b++)
-#pragma unroll
-    for (int v = 0; v < 16; v++) o[b][v] = 0.0f;
+  for (int b = 0; b < NB; b++) o[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = -INFINITY;  // log2 units
   float l_run = 0.0f;
 
@@ -148,26 +149,26 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
     for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[j];
     __syncthreads();
   }
-  // Load geometry: wave instruction g covers rows [g*RPI, g*RPI + RPI); lane -> (row, chunk).
   const int lrow = lane / C4;
   const int lpos = lane - lrow * C4;
 
   auto issue_tile = [&](int kt, float *dk, float *dv) {
 #pragma unroll
     for (int p = 0; p < LPW; p++) {
-      const int g = p * 4 + wave;
-      const int r = g * RPI + lrow;
+      const int gi = p * NW + wave;  // instruction index: rows [gi*RPI, gi*RPI + RPI)
+      const int r = gi * RPI + lrow;
       const int key = min(kt + r, it.ke - 1);  // rows past the chunk are loaded but masked
       const int64_t row = tile_row(a.kv, stab, blk0, it.kbase, key);
-      const int col = (lpos ^ (r & 7)) * 4;
-      const float *gk = kbase + row * rs + col;
-      const float *gv = vbase + row * rs + col;
+      // K chunks are XOR-swizzled by (row & 15) for the column reads of QK; V rows are read
+      // along the row, which is conflict-free unswizzled.
+      const float *gk = kbase + row * rs + (lpos ^ (r & 15)) * 4;
+      const float *gv = vbase + row * rs + lpos * 4;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void *)gk,
-          (__attribute__((address_space(3))) void *)(dk + g * RPI * D), 16, 0, 0);
+          (__attribute__((address_space(3))) void *)(dk + gi * RPI * D), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void *)gv,
-          (__attribute__((address_space(3))) void *)(dv + g * RPI * D), 16, 0, 0);
+          (__attribute__((address_space(3))) void *)(dv + gi * RPI * D), 16, 0, 0);
     }
   };
 
@@ -175,47 +176,43 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
     if (!wave_active || kt >= whi_max || kt + KT <= wlo_min) return;
     const bool full = (kt + KT <= whi_min) && (kt >= wlo_max);
 
-    // S^T = K Q^T: step s contracts dim half*DH + s; K row i, 16-byte chunk (half*DH+s)/4.
-    f32x16 st;
+    // S^T = K Q^T per 16-key block kb: A[key][k] = K[16kb + i][DQ*g + s] (lane i, g),
+    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at position c ^ i.
+    f32x4 st[2];
+    st[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    st[1] = st[0];
+    const float *kb[DQ / 4];
 #pragma unroll
-    for (int v = 0; v < 16; v++) st[v] = 0.0f;
-    const float *krow = sk + i * D;
+    for (int j = 0; j < DQ / 4; j++) kb[j] = sk + i * D + 4 * (((DQ / 4) * g + j) ^ i);
 #pragma unroll
-    for (int s = 0; s < DH; s += 4) {
-      const int c = ((half * DH + s) >> 2) ^ (i & 7);
-      const float4 kk = ld4(krow + c * 4);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.x, qr[s], st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.y, qr[s + 1], st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.z, qr[s + 2], st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kk.w, qr[s + 3], st, 0, 0, 0);
+    for (int blk = 0; blk < 2; blk++) {
+#pragma unroll
+      for (int s = 0; s < DQ; s += 4) {
+        const float4 kk = ld4(kb[s >> 2] + blk * 16 * D);
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qr[s], st[blk], 0, 0, 0);
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qr[s + 1], st[blk], 0, 0, 0);
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[s + 2], st[blk], 0, 0, 0);
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[s + 3], st[blk], 0, 0, 0);
+      }
     }
-    // Keep at most two K reads in flight ahead of the MFMAs (bounds register pressure).
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int s = 0; s < DH / 4 - 2; s++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 
-    // st[v] holds key kt + 8*(v/4) + 4*half + v%4 for query i (log2-scaled below).
+    // p[4*blk + v] holds key kt + 16*blk + 4*g + v for query i (log2-scaled).
+    float p[8];
     float mx = -INFINITY;
-    if (full) {
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        st[v] *= sl2;
-        mx = fmaxf(mx, st[v]);
-      }
-    } else {
+    for (int blk = 0; blk < 2; blk++)
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int key = kt + 8 * (v >> 2) + 4 * half + (v & 3);
-        const bool vis = key >= vis_lo && key < vis_hi;
-        st[v] = vis ? st[v] * sl2 : -INFINITY;
-        mx = fmaxf(mx, st[v]);
+      for (int v = 0; v < 4; v++) {
+        float x = st[blk][v] * sl2;
+        if (!full) {
+          const int key = kt + 16 * blk + 4 * g + v;
+          x = (key >= vis_lo && key < vis_hi) ? x : -INFINITY;
+        }
+        p[4 * blk + v] = x;
+        mx = fmaxf(mx, x);
       }
-    }
-    mx = fmaxf(mx, xor32(mx));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
     const bool need = mx > m_run + kLazyRescale;
     if (__any(need)) {
       const float mn = need ? mx : m_run;
@@ -227,38 +224,26 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
     }
     const float ms = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      st[v] = __builtin_amdgcn_exp2f(st[v] - ms);
-      l_run += st[v];
+    for (int s = 0; s < 8; s++) {
+      p[s] = __builtin_amdgcn_exp2f(p[s] - ms);
+      l_run += p[s];
     }
 
-    // O^T += V^T P^T: step s contracts key 8*(s/4) + 4*half + s%4 (= st[s] in this lane); the
-    // A operand of block b is V[key][NB*i + b], read for all blocks at once.
+    // O^T += V^T P^T: step s contracts key 16*(s/4) + 4*g + s%4 (= p[s] in this lane).  The A
+    // operand of block 4*hh + bb is V[key][64*hh + 4*i + bb], one ds_read_b128 per hh.
+    const float *vrow = sv + 4 * g * D + 4 * i;
 #pragma unroll
-    for (int s = 0; s < 16; s++) {
-      const int key = 8 * (s >> 2) + 4 * half + (s & 3);
-      const int byte = (i * NB * 4);
-      const int chunk = (byte >> 4) ^ (key & 7);
-      const float *vp = sv + key * D + chunk * 4 + ((byte & 15) >> 2);
-      if constexpr (NB == 4) {
-        const float4 vv = ld4(vp);
-        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, st[s], o[0], 0, 0, 0);
-        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, st[s], o[1], 0, 0, 0);
-        o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, st[s], o[2], 0, 0, 0);
-        o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, st[s], o[3], 0, 0, 0);
-      } else {
-        const float2 vv = *reinterpret_cast<const float2 *>(vp);
-        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, st[s], o[0], 0, 0, 0);
-        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, st[s], o[1], 0, 0, 0);
+    for (int s = 0; s < 8; s++) {
+      const float *vp = vrow + (16 * (s >> 2) + (s & 3)) * D;
+#pragma unroll
+      for (int hh = 0; hh < H64; hh++) {
+        const float4 vv = ld4(vp + 64 * hh);
+        o[4 * hh + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[s], o[4 * hh + 0], 0, 0, 0);
+        o[4 * hh + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[s], o[4 * hh + 1], 0, 0, 0);
+        o[4 * hh + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[s], o[4 * hh + 2], 0, 0, 0);
+        o[4 * hh + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[s], o[4 * hh + 3], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-#pragma unroll
-    for (int s = 0; s < 14; s++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NB, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NB, 1);
   };
 
   // Double-buffered key loop with one barrier per tile: at the barrier of tile t every wave
@@ -278,35 +263,33 @@ __global__ void __launch_bounds__(256) prefill_kernel(TileLaunch a) {
     compute_tile(kt + KT, sk1, sv1);
   }
 
-  const float l_tot = l_run + xor32(l_run);
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot += __shfl_xor(l_tot, 32);
   if (!qvalid || !wave_active) return;
-  if (it.part < 0) {
-    const float inv = l_tot == 0.0f ? 0.0f : 1.0f / l_tot;
-    float *op = a.out + ((size_t)(it.qstart + qi) * a.hq + h) * D;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int r = 8 * (v >> 2) + 4 * half + (v & 3);
-      if constexpr (NB == 4)
-        st4(op + 4 * r, make_float4(o[0][v] * inv, o[1][v] * inv, o[2][v] * inv, o[3][v] * inv));
-      else
-        *reinterpret_cast<float2 *>(op + 2 * r) = make_float2(o[0][v] * inv, o[1][v] * inv);
-    }
+  // Lane (i, g) holds O^T rows r = 4g + v of every block: dims 64*hh + 4r + bb.
+  float *op;
+  float inv = 1.0f;
+  const bool partial = it.part >= 0;
+  size_t pidx = 0;
+  if (!partial) {
+    inv = l_tot == 0.0f ? 0.0f : 1.0f / l_tot;
+    op = a.out + ((size_t)(it.qstart + qi) * a.hq + h) * D;
   } else {
     // Partial of one key chunk: rows of the tile are laid out query-major, chunk-minor.
-    const size_t p = ((size_t)it.part + (size_t)(qi - it.q0) * it.nsplit + it.split) * a.hq + h;
-    float *op = a.part_acc + p * D;
+    pidx = ((size_t)it.part + (size_t)(qi - it.q0) * it.nsplit + it.split) * a.hq + h;
+    op = a.part_acc + pidx * D;
+  }
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int r = 8 * (v >> 2) + 4 * half + (v & 3);
-      if constexpr (NB == 4)
-        st4(op + 4 * r, make_float4(o[0][v], o[1][v], o[2][v], o[3][v]));
-      else
-        *reinterpret_cast<float2 *>(op + 2 * r) = make_float2(o[0][v], o[1][v]);
-    }
-    if (half == 0) {
-      a.part_m[p] = m_run;
-      a.part_l[p] = l_tot;
-    }
+  for (int v = 0; v < 4; v++) {
+    const int r = 4 * g + v;
+#pragma unroll
+    for (int hh = 0; hh < H64; hh++)
+      st4(op + 64 * hh + 4 * r, make_float4(o[4 * hh][v] * inv, o[4 * hh + 1][v] * inv,
+                                          o[4 * hh + 2][v] * inv, o[4 * hh + 3][v] * inv));
+  }
+  if (partial && g == 0) {
+    a.part_m[pidx] = m_run;
+    a.part_l[pidx] = l_tot;
   }
 }
 
@@ -316,9 +299,10 @@ template <int D>
 hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
   const dim3 grid(a.num_items, a.hkv * ((a.hq / a.hkv) / hpw));
   switch (hpw) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(512), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(512), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4>), grid, dim3(512), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8>), grid, dim3(512), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -328,7 +312,7 @@ hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
 
 bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
   return (head_dim == 64 || head_dim == 128) &&
-         (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4);
+         (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8);
 }
 
 hipError_t launch_prefill_tiles(const TileLaunch &a, int hpw, hipStream_t s) {
