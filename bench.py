@@ -43,7 +43,36 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work budget of the baseline")
     ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device-to-device copy three times (the "
+                         "known-size reference for the FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+COPY_BYTES = 1 << 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def copy_calibration():
+    import torch
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 x {COPY_BYTES} bytes device-to-device")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE/WRITE_SIZE summary, each
+    counter scaled by what it reads for a plain copy of known size; None if not measured."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)[kernel]
+        return int(round(t["bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def log(msg):
@@ -143,7 +172,8 @@ def bench_decode(args, ctx):
         "wl": wl, "ms": ms, "bytes": byts, "gbs": byts / (ms * 1e-3) / 1e9,
         "kernel_ms": {n: s[1] / max(s[0], 1) for n, s in stats.items() if s[0]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("decode"),
                      "kernel": "row_attention_kernel<128,2> (split-KV decode)",
                      "algorithmic_bytes_per_launch": byts},
     }
@@ -183,7 +213,8 @@ def bench_prefill(args, ctx):
         "kernel_ms": {n: round(s[1] / max(s[0], 1), 5) for n, s in stats.items() if s[0]},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("prefill"),
                      "kernel": "prefill_kernel<128,2> (fp32 MFMA 16x16x4, 8 waves)",
                      "algorithmic_flops_per_launch": flops},
     }
@@ -271,6 +302,8 @@ def main():
     if args.only in (None, "prefill"):
         pf = bench_prefill(args, ctx)
     ctx.close()
+    if args.copy_calibration:
+        copy_calibration()
     cpu = None
     if dec is not None and not args.no_cpu:
         cpu = cpu_baseline(dec["wl"], args.cpu_seconds)
