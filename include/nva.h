@@ -63,6 +63,15 @@ typedef struct nva_attn_desc {
   int32_t write_kv;
 } nva_attn_desc;
 
+/* RMSNorm(weight, eps, onePlusWeight) and RMSNorm.weightless(eps), layers/Norms.java:32-97.
+ * weight is a DEVICE pointer to [width] fp32 (the model's resident norm weight), or NULL for
+ * the weightless norm (identity gain).  one_plus_weight applies (1 + w) (Gemma 3). */
+typedef struct nva_rms_norm {
+  const float *weight;
+  float eps;
+  int32_t one_plus_weight;
+} nva_rms_norm;
+
 /* ------------------------------------------------------------------ context
  * Replaces the per-LLM engine objects that Transformer builds and closes
  * (engine/Transformer.java:113-143, 257-271). */
@@ -165,6 +174,29 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
                                       const nva_attn_desc *desc, const float *q,
                                       const float *k, const float *v, int num_tokens,
                                       float *q_out, float *k_out, float *out);
+
+/* RMSNorm.forward(x), layers/Norms.java:91-96 -> Ops.rmsNorm, tensor/Ops.java:444-500, over
+ * x [rows, width] (device) into out [rows, width] (device; may equal x).  The sum of squares
+ * follows ScalarFloatKernels.sumSquares (scalar/ScalarFloatKernels.java:55-70) bit for bit;
+ * inv = (float)(1.0 / Math.sqrt(sum / width + eps)) in double. */
+nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const float *x, int rows,
+                                int width, float *out);
+
+/* The per-head q/k (and Gemma 4 v) RMSNorm, RotaryEmbedding.forward and Attention.forward as
+ * one call, the way the model layers chain them (Qwen3Attention.forward,
+ * models/internal/Qwen3ForCausalLM.java:207-227 normHeads; Gemma3ForCausalLM.java:143-157;
+ * Gemma4ForCausalLM.java:164-197 with its weightless v norm): one fused kernel normalises each
+ * head row, rotates q and k, and stores rotated k and normalised v into the pages; then the
+ * attention kernels run.  q_norm / k_norm / v_norm may each be NULL (no norm on that tensor).
+ * q_out/k_out (may be NULL) receive the normalised, rotated q and k.  Results are identical to
+ * nva_rms_norm_forward on each head row, then nva_rope_attention_forward. */
+nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                           const nva_rms_norm *q_norm,
+                                           const nva_rms_norm *k_norm,
+                                           const nva_rms_norm *v_norm,
+                                           const nva_attn_desc *desc, const float *q,
+                                           const float *k, const float *v, int num_tokens,
+                                           float *q_out, float *k_out, float *out);
 
 #ifdef __cplusplus
 }

@@ -163,6 +163,7 @@ struct nva_ctx {
   DevBuf d_part;     // split partials
   DevBuf d_q_rot;    // fused path scratch for rotated q
   DevBuf d_k_rot;    // fused path scratch for rotated k
+  DevBuf d_v_norm;   // fused path scratch for normalised v (dense prefill with a v norm)
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
 
   bool timing = false;
@@ -718,6 +719,19 @@ nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &
 }
 
 // Math.round(float), Norms.java:317: floor(x + 1/2) evaluated exactly; NaN -> 0; saturating.
+// The kernels' view of an RMSNorm descriptor; NULL disables the norm.  Any eps is accepted, as
+// in the reference (a negative var + eps gives NaN there too).
+HeadNorm head_norm(const nva_rms_norm *n) {
+  HeadNorm h{};
+  if (n) {
+    h.weight = n->weight;
+    h.eps = n->eps;
+    h.enabled = 1;
+    h.one_plus = n->one_plus_weight ? 1 : 0;
+  }
+  return h;
+}
+
 int32_t java_round(float x) {
   if (std::isnan(x)) return 0;
   const float f = std::floor(x);
@@ -785,6 +799,7 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   ctx->d_part.release();
   ctx->d_q_rot.release();
   ctx->d_k_rot.release();
+  ctx->d_v_norm.release();
   ctx->d_gather.release();
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
@@ -1183,6 +1198,17 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
                                       const nva_attn_desc *desc, const float *q,
                                       const float *k, const float *v, int num_tokens,
                                       float *q_out, float *k_out, float *out) {
+  return nva_norm_rope_attention_forward(ctx, kv, rope, nullptr, nullptr, nullptr, desc, q, k, v,
+                                         num_tokens, q_out, k_out, out);
+}
+
+nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                           const nva_rms_norm *q_norm,
+                                           const nva_rms_norm *k_norm,
+                                           const nva_rms_norm *v_norm,
+                                           const nva_attn_desc *desc, const float *q,
+                                           const float *k, const float *v, int num_tokens,
+                                           float *q_out, float *k_out, float *out) {
   if (!ctx) return NVA_E_ARG;
   nva_status st = check_forward(ctx, kv, desc, num_tokens);
   if (st != NVA_OK) return st;
@@ -1209,6 +1235,12 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
     HIP_TRY(ctx, ctx->d_k_rot.reserve(kn * 4 + 16), "rotated k scratch");
     k_out = static_cast<float *>(ctx->d_k_rot.ptr);
   }
+  // Dense prefill attends over the step's own k/v rows, so a normalised v must exist as rows.
+  float *v_out = nullptr;
+  if (v_norm && dense) {
+    HIP_TRY(ctx, ctx->d_v_norm.reserve(kn * 4 + 16), "normalised v scratch");
+    v_out = static_cast<float *>(ctx->d_v_norm.ptr);
+  }
   const bool store = d.write_kv && kv->k[layer] && ctx->has_slots &&
                      ctx->num_slots == num_tokens;
   if (store) {
@@ -1221,6 +1253,7 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
   a.v = v;
   a.q_out = q_out;
   a.k_out = k_out;
+  a.v_out = v_out;
   a.k_cache = store ? kv->k[layer] : nullptr;
   a.v_cache = store ? kv->v[layer] : nullptr;
   a.slots = store ? ctx->dev_i32(ctx->off_slots) : nullptr;
@@ -1230,12 +1263,36 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
   a.hq = d.num_heads;
   a.hk = d.num_kv_heads;
   a.head_dim = d.head_dim;
+  a.qn = head_norm(q_norm);
+  a.kn = head_norm(k_norm);
+  a.vn = head_norm(v_norm);
+  if (rope_store_norm_lds(a) > kRopeNormMaxLds)
+    return fail(ctx, NVA_E_UNSUPPORTED, "head norms of %d+2*%d heads of %d floats exceed the "
+                "kernel's %zu-byte LDS budget", a.hq, a.hk, a.head_dim, kRopeNormMaxLds);
   {
     Timed tm(ctx, "rope_store");
     HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "rope_store kernel launch");
     tm.done();
   }
-  return attention_after_store(ctx, kv, d, q_out, k_out, v, num_tokens, out);
+  return attention_after_store(ctx, kv, d, q_out, k_out, v_out ? v_out : v, num_tokens, out);
+}
+
+nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const float *x, int rows,
+                                int width, float *out) {
+  if (!ctx) return NVA_E_ARG;
+  if (!norm) return fail(ctx, NVA_E_ARG, "RMSNorm descriptor is null");
+  if (rows < 0 || width <= 0) return fail(ctx, NVA_E_ARG, "bad shape [%d, %d]", rows, width);
+  if (rows > 0 && (!x || !out)) return fail(ctx, NVA_E_ARG, "x and out are required");
+  NormLaunch a{};
+  a.x = x;
+  a.out = out;
+  a.norm = head_norm(norm);
+  a.rows = rows;
+  a.width = width;
+  Timed tm(ctx, "rms_norm");
+  HIP_TRY(ctx, launch_rms_norm(a, ctx->stream), "rms_norm kernel launch");
+  tm.done();
+  return NVA_OK;
 }
 
 }  // extern "C"

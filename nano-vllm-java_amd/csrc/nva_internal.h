@@ -88,14 +88,33 @@ struct TileLaunch {
   float *part_m, *part_l, *part_acc;  // split tiles: [P, Hq], [P, Hq], [P, Hq, D]
 };
 
+// RMSNorm of every head row of one tensor (RMSNorm.forward over [T*H, d], Ops.java:444-500).
+struct HeadNorm {
+  const float *weight;  // [d], or null: weightless (identity gain)
+  float eps;
+  int32_t enabled;
+  int32_t one_plus;     // apply (1 + w)
+  int32_t pad;
+};
+
 struct RopeStoreLaunch {
   const float *q, *k, *v;     // inputs [T, hq, d], [T, hk, d], [T, hk, d]; k/v may be null
   float *q_out, *k_out;       // rotated outputs (k_out may be null)
+  float *v_out;               // normalised v [T, hk, d] (only with a v norm; may be null)
   float *k_cache, *v_cache;   // store targets (null: no store)
   const int32_t *slots;       // [T] or null
   const int32_t *positions;   // [T] rounded, validated positions (null: no rotation)
   const float *cos_sin;       // [max_pos, d]
   int32_t tokens, hq, hk, head_dim;
+  HeadNorm qn, kn, vn;        // per-head RMSNorm applied to q, k, v before rotation / store
+};
+
+// Standalone RMSNorm over rows of any width (RMSNorm.forward).
+struct NormLaunch {
+  const float *x;
+  float *out;
+  HeadNorm norm;
+  int32_t rows, width;
 };
 
 struct GatherLaunch {
@@ -107,6 +126,10 @@ struct GatherLaunch {
 
 // Kernel launchers (each returns the hipGetLastError() of its launch).
 hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s);
+hipError_t launch_rms_norm(const NormLaunch &a, hipStream_t s);
+// LDS bytes the fused kernel needs for its head norms (0 when no norm is enabled).
+size_t rope_store_norm_lds(const RopeStoreLaunch &a);
+constexpr size_t kRopeNormMaxLds = 64 * 1024;
 hipError_t launch_gather(const GatherLaunch &a, hipStream_t s);
 hipError_t launch_row_attention(const RowLaunch &a, int heads_per_wg, hipStream_t s);
 hipError_t launch_merge(const MergeLaunch &a, hipStream_t s);

@@ -11,6 +11,7 @@ from .layers import (  # noqa: F401
     KvCacheArena,
     NullPointerException,
     NvaError,
+    RMSNorm,
     RotaryEmbedding,
     UnsupportedShapeError,
 )

@@ -47,6 +47,19 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class RmsNormDesc(ctypes.Structure):
+    """nva_rms_norm: RMSNorm(weight, eps, onePlusWeight) (layers/Norms.java:32-97); weight is a
+    device pointer or None (weightless)."""
+
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("one_plus_weight", ctypes.c_int32),
+    ]
+
+
+_pnorm = ctypes.POINTER(RmsNormDesc)
+
 SIGNATURES = {
     "nva_ctx_create": ([_ci, _pvp], _st),
     "nva_ctx_destroy": ([_vp], _st),
@@ -75,6 +88,10 @@ SIGNATURES = {
     "nva_attention_forward": ([_vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci, _vp], _st),
     "nva_rope_attention_forward": ([_vp, _vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci,
                                     _vp, _vp, _vp], _st),
+    "nva_rms_norm_forward": ([_vp, _pnorm, _vp, _ci, _ci, _vp], _st),
+    "nva_norm_rope_attention_forward": ([_vp, _vp, _vp, _pnorm, _pnorm, _pnorm,
+                                         ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci, _vp, _vp,
+                                         _vp], _st),
 }
 
 _lib = None

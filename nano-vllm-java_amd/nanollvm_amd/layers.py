@@ -8,6 +8,8 @@ the reference's own code:
 * ``KvCacheArena``   -- engine/KvCacheArena.java (per-layer K/V pages, resident in HBM).
 * ``RotaryEmbedding``-- layers/Norms.java:158-388 (cos|sin table, ``forward``).
 * ``Attention``      -- layers/Attention.java (constructor arguments, ``forward``).
+* ``RMSNorm``        -- layers/Norms.java:32-97 (``forward``; ``weightless``), applied per head
+                        by the model layers before RoPE.
 
 (Reference paths are relative to nano-vllm-java/src/main/java/com/igormaznitsa/nanollvm/.)
 Tensors are torch CUDA float32 tensors (device memory only; torch does no compute here).  Java
@@ -338,6 +340,43 @@ class RotaryEmbedding:
             self._h = None
 
 
+class RMSNorm:
+    """RMSNorm(weight, eps, onePlusWeight) / RMSNorm.weightless(eps) (Norms.java:32-97).
+
+    ``weight`` is a float32 device tensor of the normalised width (kept resident, as the model's
+    weights are); ``None`` is the weightless norm."""
+
+    def __init__(self, weight: Optional[torch.Tensor], eps: float,
+                 one_plus_weight: bool = False):
+        if weight is not None and weight.dim() != 1:
+            raise IllegalArgumentException("RMSNorm weight must be 1-D")
+        self.weight = weight
+        self.eps = float(np.float32(eps))
+        self.one_plus_weight = bool(one_plus_weight)
+        self._desc = N.RmsNormDesc(None if weight is None else _dev(weight, "weight"), self.eps,
+                                   int(self.one_plus_weight))
+
+    @staticmethod
+    def weightless(eps: float) -> "RMSNorm":
+        return RMSNorm(None, eps)
+
+    def desc(self):
+        return ctypes.byref(self._desc)
+
+    def forward(self, x: torch.Tensor, ctx: "Context") -> torch.Tensor:
+        """RMSNorm.forward(x): normalises x along its last axis into a new tensor."""
+        width = x.shape[-1]
+        if self.weight is not None and self.weight.numel() != width:
+            raise IllegalArgumentException(
+                f"weight has {self.weight.numel()} entries, last dimension is {width}")
+        out = torch.empty_like(x)
+        rows = x.numel() // width if width else 0
+        _check(ctx.handle, N.load().nva_rms_norm_forward(
+            ctx.handle, self.desc(), _dev(x, "x"), rows, width, _dev(out, "out")),
+            "RMSNorm.forward")
+        return out
+
+
 class Attention:
     """Attention(numHeads, headDim, scale, numKvHeads, slidingWindow, kvLayerIndex, writeKv)
     (Attention.java:70-125)."""
@@ -399,4 +438,35 @@ class Attention:
             ctypes.byref(self._desc), _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), q.shape[0],
             _dev(q_out, "q_out"), _dev(k_out, "k_out"), _dev(out, "out")),
             "Attention.forward_with_rope")
+        return out
+
+    def forward_with_norm_rope(self, rope: RotaryEmbedding, positions, q: torch.Tensor,
+                               k: torch.Tensor, v: torch.Tensor, ctx: Context,
+                               q_norm: Optional[RMSNorm] = None,
+                               k_norm: Optional[RMSNorm] = None,
+                               v_norm: Optional[RMSNorm] = None,
+                               q_out: Optional[torch.Tensor] = None,
+                               k_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """normHeads(q, qNorm), normHeads(k, kNorm) [, vNorm(v)], RotaryEmbedding.forward and
+        Attention.forward as one call (Qwen3ForCausalLM.java:207-227, Gemma3ForCausalLM.java:
+        143-157, Gemma4ForCausalLM.java:164-197): one fused kernel normalises, rotates and
+        stores, then the attention kernels run."""
+        self._check_shapes(q, k, v)
+        for t, shape in ((q_out, q.shape), (k_out, k.shape)):
+            if t is not None and tuple(t.shape) != tuple(shape):
+                raise IllegalArgumentException("q_out/k_out must match q/k")
+        for n in (q_norm, k_norm, v_norm):
+            if n is not None and n.weight is not None and n.weight.numel() != self.head_dim:
+                raise IllegalArgumentException("head norm weights must have headDim entries")
+        if positions is not None:
+            ctx.set_positions(positions)
+        arena = ctx.kv_cache()
+        out = torch.empty((q.shape[0], self.num_heads, self.head_dim), dtype=torch.float32,
+                          device=q.device)
+        _check(ctx.handle, N.load().nva_norm_rope_attention_forward(
+            ctx.handle, arena.handle if arena is not None else None, rope.handle,
+            None if q_norm is None else q_norm.desc(), None if k_norm is None else k_norm.desc(),
+            None if v_norm is None else v_norm.desc(), ctypes.byref(self._desc), _dev(q, "q"),
+            _dev(k, "k"), _dev(v, "v"), q.shape[0], _dev(q_out, "q_out"), _dev(k_out, "k_out"),
+            _dev(out, "out")), "Attention.forward (q/k norm + RoPE)")
         return out

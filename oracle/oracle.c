@@ -20,6 +20,9 @@
  *   tensor/scalar/ScalarFloatKernels.java:27-42,164-182   dot/scale/axpy (kernels mode 0)
  *   tensor/vector/VectorFloatKernels.java:57-87,285-317   dot/scale/axpy (kernels mode LANE)
  *   tensor/MatmulRuntime.java:194-225                     parallelRanges (threads > 1)
+ *   tensor/Ops.java:444-500         rmsNorm (weightless / weight / onePlusWeight) -> orc_rms_norm()
+ *   tensor/scalar/ScalarFloatKernels.java:45-80           sumSquares/scaleAdd/scaleAddOnePlus
+ *   tensor/vector/VectorFloatKernels.java:90-156          sumSquares/scaleAdd/scaleAddOnePlus
  *
  * Build with -ffp-contract=off: every float operation below is a separately rounded IEEE op,
  * as in Java, and an explicit fmaf() stands wherever Java calls FloatVector.fma.
@@ -48,6 +51,10 @@
 #define MUT_WINDOW_OFF1 4    /* sliding window one key too wide */
 #define MUT_NO_RESCALE 5     /* acc not multiplied by alpha between tiles */
 #define MUT_ROPE_SIGN 6      /* rotate-half with the sign of the sin term flipped */
+#define MUT_NORM_NO_EPS 7    /* rmsNorm without eps under the root */
+#define MUT_NORM_DIV_N1 8    /* mean of squares divided by n - 1 */
+#define MUT_NORM_PAIRWISE 9  /* sumSquares summed as a pairwise tree, not in the scalar order */
+#define MUT_NORM_NO_ONE 10   /* onePlusWeight ignored (w instead of 1 + w) */
 
 typedef struct {
   int num_heads;
@@ -194,6 +201,96 @@ int orc_rope_forward(const float *table, int max_pos, int head_size, const float
     }
   }
   return ORC_OK;
+}
+
+/* ---------------------------------------------------------------- RMSNorm (q/k/v head norms) */
+
+/* ScalarFloatKernels.sumSquares, ScalarFloatKernels.java:55-70: groups of four summed left to
+ * right, ((v0*v0 + v1*v1) + v2*v2) + v3*v3, each group added to the running sum in order, then
+ * the tail element by element. */
+static float sum_squares_scalar(const float *a, int n) {
+  float sum = 0.0f;
+  int i = 0;
+  for (; i + 4 <= n; i += 4) {
+    float t = a[i] * a[i];
+    t = t + a[i + 1] * a[i + 1];
+    t = t + a[i + 2] * a[i + 2];
+    t = t + a[i + 3] * a[i + 3];
+    sum = sum + t;
+  }
+  for (; i < n; i++) sum = sum + a[i] * a[i];
+  return sum;
+}
+
+/* VectorFloatKernels.sumSquares with LANE lanes, VectorFloatKernels.java:90-119: four FMA
+ * accumulators over spans of 4*LANE, leftover whole vectors into acc0, (acc0+acc1)+(acc2+acc3),
+ * reduceLanes (order unspecified by the JDK: a pairwise tree here), then the scalar tail. */
+static float sum_squares_vector(const float *a, int n, int lane) {
+  float acc[4][16];
+  memset(acc, 0, sizeof(acc));
+  int upper = n - n % lane;
+  int span = lane * 4;
+  int ubound = upper - upper % span;
+  int i = 0;
+  for (; i < ubound; i += span)
+    for (int r = 0; r < 4; r++)
+      for (int j = 0; j < lane; j++) {
+        float v = a[i + r * lane + j];
+        acc[r][j] = fmaf(v, v, acc[r][j]);
+      }
+  for (; i < upper; i += lane)
+    for (int j = 0; j < lane; j++) acc[0][j] = fmaf(a[i + j], a[i + j], acc[0][j]);
+  float red[16];
+  for (int j = 0; j < lane; j++) red[j] = (acc[0][j] + acc[1][j]) + (acc[2][j] + acc[3][j]);
+  for (int w = lane / 2; w >= 1; w /= 2)
+    for (int j = 0; j < w; j++) red[j] = red[j] + red[j + w];
+  float sum = red[0];
+  for (; i < n; i++) sum = sum + a[i] * a[i];
+  return sum;
+}
+
+/* Planted order mistake: squares summed as a pairwise tree. */
+static float sum_squares_pairwise(const float *a, int n) {
+  float buf[4096];
+  int m = n < 4096 ? n : 4096;
+  for (int i = 0; i < m; i++) buf[i] = a[i] * a[i];
+  while (m > 1) {
+    int h = (m + 1) / 2;
+    for (int i = 0; i + h < m; i++) buf[i] = buf[i] + buf[i + h];
+    m = h;
+  }
+  return n > 0 ? buf[0] : 0.0f;
+}
+
+/* VectorMath.sumSquares with the chosen backend (mode 0 scalar, else Vector API lanes). */
+float orc_sum_squares(const float *a, int n, int mode, int mutation) {
+  if (mutation == MUT_NORM_PAIRWISE) return sum_squares_pairwise(a, n);
+  return mode == 0 ? sum_squares_scalar(a, n) : sum_squares_vector(a, n, mode);
+}
+
+/* Ops.rmsNorm(x, eps) and Ops.rmsNorm(x, weight, eps, onePlusWeight), Ops.java:444-500, over
+ * rows of `width` floats: var = sumSquares / width (float division), inv =
+ * (float)(1.0 / Math.sqrt(var + eps)) with var + eps a float sum widened to double, then
+ * out = x * inv (weightless, VectorMath.scale), x * inv * w (scaleAdd) or x * inv * (1 + w)
+ * (scaleAddOnePlus), each product separately rounded, left to right. */
+void orc_rms_norm(const float *x, int rows, int width, const float *weight, float eps,
+                  int one_plus, int mode, int mutation, float *out) {
+  for (int r = 0; r < rows; r++) {
+    const float *xr = x + (size_t)r * width;
+    float *o = out + (size_t)r * width;
+    float sum = orc_sum_squares(xr, width, mode, mutation);
+    float var = sum / (float)(mutation == MUT_NORM_DIV_N1 ? width - 1 : width);
+    float ve = mutation == MUT_NORM_NO_EPS ? var : var + eps;
+    float inv = (float)(1.0 / sqrt((double)ve));
+    for (int i = 0; i < width; i++) {
+      float y = xr[i] * inv;
+      if (weight) {
+        float w = one_plus && mutation != MUT_NORM_NO_ONE ? 1.0f + weight[i] : weight[i];
+        y = y * w;
+      }
+      o[i] = y;
+    }
+  }
 }
 
 /* ---------------------------------------------------------------- store (a2) */

@@ -36,6 +36,15 @@ How each oracle function is pinned (the tests named here live in ``tests/test_or
   The reference's own attention tests pin only parallel-vs-sequential self-consistency
   (T/CoreUnitTest.java:1462-1471); that test is re-expressed here too (threads 1 vs 2 must be
   bit-identical).
+* ``sum_squares`` / ``rms_norm`` -- ``tests/test_oracle_norm.py``: against the float64 textbook
+  ``rms_norm_fp64`` within 2e-6 relative over widths 4..1024 (weightless, weight, onePlusWeight);
+  a hand-derived known answer that fixes the scalar summation order ([4096, 1, 1, 1] sums to
+  exactly 2^24 because each +1 is a round-to-even tie, while a pairwise tree gives 2^24 + 2);
+  exact scale invariance (norm(2x) == norm(x) bit for bit with eps = 0); and the reference's
+  own tests re-expressed (T/CoreUnitTest.java:332-349 rows [1.5,1.5] and [4,4] normalise to 1;
+  :1047-1056 onePlusWeight equals the plain norm times (1 + w); :675 scalar and vector
+  sumSquares of 0.1*i agree within 1e-3).  Planted mistakes (no eps, divide by n - 1,
+  pairwise order, onePlusWeight ignored) each fail one of them.
 * ``store_kv`` -- closed form: ``cache[slot] == k[i]`` for slot >= 0, untouched elsewhere.
 
 Not pinned: the exact bits of Java's ``Math.exp`` and of ``FloatVector.reduceLanes`` (the
@@ -70,6 +79,10 @@ MUT_CAUSAL_OFF1 = 3
 MUT_WINDOW_OFF1 = 4
 MUT_NO_RESCALE = 5
 MUT_ROPE_SIGN = 6
+MUT_NORM_NO_EPS = 7
+MUT_NORM_DIV_N1 = 8
+MUT_NORM_PAIRWISE = 9
+MUT_NORM_NO_ONE = 10
 
 
 class _Attn(ctypes.Structure):
@@ -117,6 +130,10 @@ def lib():
         L.orc_rope_table.restype = None
         L.orc_rope_forward.argtypes = [vp, ci, ci, vp, vp, vp, vp, vp, ci, ci, ci, ci]
         L.orc_rope_forward.restype = ci
+        L.orc_sum_squares.argtypes = [vp, ci, ci, ci]
+        L.orc_sum_squares.restype = cf
+        L.orc_rms_norm.argtypes = [vp, ci, ci, vp, cf, ci, ci, ci, vp]
+        L.orc_rms_norm.restype = None
         L.orc_store_kv.argtypes = [vp, vp, vp, ci, ci, vp, vp]
         L.orc_store_kv.restype = None
         L.orc_attention_forward.argtypes = [
@@ -185,6 +202,40 @@ def rope_fp64(table: np.ndarray, positions, x: np.ndarray) -> np.ndarray:
     x = x.astype(np.float64)
     x1, x2 = x[..., :half], x[..., half:]
     return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+
+
+# --------------------------------------------------------------------------------------- RMSNorm
+
+def sum_squares(a, mode: int = 0, mutation: int = MUT_NONE) -> float:
+    """VectorMath.sumSquares with the scalar (mode 0) or Vector API (8/16 lanes) backend."""
+    a = _f32(a).reshape(-1)
+    return float(np.float32(lib().orc_sum_squares(_p(a), a.size, int(mode), int(mutation))))
+
+
+def rms_norm(x, weight=None, eps: float = 1e-6, one_plus: bool = False, mode: int = 0,
+             mutation: int = MUT_NONE) -> np.ndarray:
+    """Ops.rmsNorm over the last axis of x (any leading shape).  mode 0 = scalar kernels
+    (ScalarFloatKernels.sumSquares order), 8 or 16 = Vector API lanes."""
+    x = _f32(x)
+    width = x.shape[-1]
+    rows = x.size // width if width else 0
+    w = None if weight is None else _f32(weight).reshape(-1)
+    if w is not None and w.size != width:
+        raise ValueError("weight length must equal the last dimension")
+    out = np.zeros_like(x)
+    lib().orc_rms_norm(_p(x), rows, width, _p(w), float(np.float32(eps)), int(bool(one_plus)),
+                       int(mode), int(mutation), _p(out))
+    return out
+
+
+def rms_norm_fp64(x, weight=None, eps: float = 1e-6, one_plus: bool = False) -> np.ndarray:
+    """Textbook x / sqrt(mean(x^2) + eps) * w in float64."""
+    x = np.asarray(x, np.float64)
+    y = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + float(np.float32(eps)))
+    if weight is not None:
+        w = np.asarray(weight, np.float64)
+        y = y * (1.0 + w if one_plus else w)
+    return y
 
 
 # ------------------------------------------------------------------------------------- attention

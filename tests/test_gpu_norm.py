@@ -1,0 +1,167 @@
+"""Parity of the per-head RMSNorm (standalone and fused with RoPE + store + attention) on the
+GPU, through the C ABI, against the CPU oracle.
+
+Bar: normalised, rotated q/k and every page byte bit-exact (the norm follows the reference's
+scalar sumSquares order); attention outputs within max-abs 1e-4 and rel-L2 1e-5."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from cases import Case, rel_l2, small_cases
+from nanollvm_amd import Attention, Context, KvCacheArena, RMSNorm, RotaryEmbedding
+from nanollvm_amd import workloads as W
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 1e-4
+REL_L2 = 1e-5
+EPS = 1e-6
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("width", [3, 7, 128, 256, 1024, 4100])
+@pytest.mark.parametrize("kind", ["weightless", "weight", "one_plus"])
+def test_rms_norm_bit_exact(ctx, width, kind):
+    say(f"rms_norm width={width} {kind}")
+    rng = np.random.default_rng(width + len(kind))
+    x = (rng.standard_normal((37, width)) * 3.0).astype(np.float32)
+    w = None if kind == "weightless" else rng.standard_normal(width).astype(np.float32)
+    norm = RMSNorm(None if w is None else dev(w), EPS, kind == "one_plus")
+    got = norm.forward(dev(x), ctx)
+    ctx.sync()
+    want = O.rms_norm(x, w, EPS, kind == "one_plus")
+    diff = bits(got.cpu().numpy()) != bits(want)
+    assert not diff.any(), f"{int(diff.sum())} of {diff.size} elements differ"
+
+
+def test_rms_norm_order_known_answer(ctx):
+    """[4096, 1, 1, 1]: the scalar order gives sum 2^24 exactly (a pairwise or lane-split order
+    gives 2^24 + 2), so the output pins the summation order on the device too."""
+    x = np.zeros((1, 128), np.float32)
+    x[0, :4] = [4096.0, 1.0, 1.0, 1.0]
+    got = RMSNorm.weightless(0.0).forward(dev(x), ctx).cpu().numpy()
+    inv = np.float32(1.0 / np.sqrt(2.0 ** 17))
+    assert got[0, 1] == inv and got[0, 0] == np.float32(np.float32(4096.0) * inv)
+
+
+def _norm_heads(x, w, one_plus):
+    return O.rms_norm(x.reshape(-1, x.shape[-1]), w, EPS, one_plus).reshape(x.shape)
+
+
+def check_fused(ctx, case, name, q_w, k_w, one_plus=False, v_norm=False, max_pos=None,
+                theta=1e4):
+    wl = case.wl
+    say(f"{name}: tokens={wl.tokens} hq={wl.hq} hkv={wl.hkv} d={wl.d} W={wl.window} "
+        f"one_plus={one_plus} v_norm={v_norm}")
+    max_pos = max_pos or 512
+    table = O.rope_table(wl.d, max_pos, theta)
+    rope = RotaryEmbedding(ctx, wl.d, wl.d, max_pos, theta, cos_sin=table)
+    if case.paged:
+        arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+        arena.write(0, 0, case.k_cache)
+        arena.write(0, 1, case.v_cache)
+    else:
+        arena = KvCacheArena(ctx, 1, 2, 16, wl.hkv, wl.d)
+    try:
+        ctx.set(**wl.meta.context_args())
+        ctx.bind_kv_cache(arena)
+        attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
+        qn = RMSNorm(None if q_w is None else dev(q_w), EPS, one_plus)
+        kn = RMSNorm(None if k_w is None else dev(k_w), EPS, one_plus)
+        vn = RMSNorm.weightless(EPS) if v_norm else None
+        q_out = torch.empty(case.q.shape, dtype=torch.float32, device="cuda")
+        k_out = torch.empty(case.k.shape, dtype=torch.float32, device="cuda")
+        out = attn.forward_with_norm_rope(rope, wl.meta.positions, dev(case.q), dev(case.k),
+                                          dev(case.v), ctx, q_norm=qn, k_norm=kn, v_norm=vn,
+                                          q_out=q_out, k_out=k_out)
+        # Oracle chain: normHeads(q), normHeads(k) [, vNorm(v)], RoPE, Attention.forward.
+        nq = _norm_heads(case.q, q_w, one_plus)
+        nk = _norm_heads(case.k, k_w, one_plus)
+        qr, kr = O.rope_forward(table, wl.meta.positions, nq, nk)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(q_out.cpu().numpy()), bits(qr)), "q not bit-exact"
+        assert np.array_equal(bits(k_out.cpu().numpy()), bits(kr)), "k not bit-exact"
+        case.q, case.k = qr, kr
+        if v_norm:
+            case.v = _norm_heads(case.v, None, False)
+        want, kc, vc = case.oracle(threads=8)
+        got = out.cpu().numpy()
+        err = float(np.max(np.abs(got - want))) if got.size else 0.0
+        rl2 = rel_l2(got, want)
+        say(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+        assert np.all(np.isfinite(got))
+        assert err <= MAX_ABS and rl2 <= REL_L2, (err, rl2)
+        if case.paged:
+            assert np.array_equal(bits(arena.get_key_cache(0)), bits(kc)), "K pages differ"
+            assert np.array_equal(bits(arena.get_value_cache(0)), bits(vc)), "V pages differ"
+    finally:
+        ctx.clear()
+        arena.close()
+        rope.close()
+
+
+SMALL = small_cases()
+
+
+@pytest.mark.parametrize("name", ["prefill_cache", "decode_gqa", "prefill_dense",
+                                  "decode_mqa_window", "prefill_cache_window"])
+@pytest.mark.parametrize("mode", ["qwen3", "gemma3", "gemma4"])
+def test_fused_norm_small(ctx, name, mode):
+    wl = SMALL[name]
+    rng = np.random.default_rng(5)
+    qw = rng.standard_normal(wl.d).astype(np.float32)
+    kw = rng.standard_normal(wl.d).astype(np.float32)
+    check_fused(ctx, Case(wl, seed=43), f"norm {mode} {name}", qw, kw,
+                one_plus=mode == "gemma3", v_norm=mode == "gemma4")
+
+
+def test_fused_norm_qwen3_prefill_full_size(ctx):
+    """Qwen3-0.6B varlen prefill 512/1024/1536/2048 (4 cached pages on the last sequence) with
+    q_norm/k_norm weights, RoPE theta 1e6."""
+    wl = W.qwen3_prefill()
+    rng = np.random.default_rng(6)
+    qw = (1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    kw = (1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    check_fused(ctx, Case(wl, seed=0), "norm qwen3 prefill", qw, kw, max_pos=wl.max_pos,
+                theta=wl.rope_theta)
+
+
+def test_fused_norm_qwen3_decode_full_size(ctx):
+    wl = W.qwen3_decode_small()
+    rng = np.random.default_rng(7)
+    qw = (1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    kw = (1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    check_fused(ctx, Case(wl, seed=0), "norm qwen3 decode B=8", qw, kw, max_pos=wl.max_pos,
+                theta=wl.rope_theta)
+
+
+def test_fused_norm_gemma3_decode_full_size(ctx):
+    wl = W.gemma3_decode(local=True)
+    rng = np.random.default_rng(8)
+    qw = (0.1 * rng.standard_normal(256)).astype(np.float32)
+    kw = (0.1 * rng.standard_normal(256)).astype(np.float32)
+    check_fused(ctx, Case(wl, seed=0), "norm gemma3 local decode", qw, kw, one_plus=True,
+                max_pos=wl.max_pos, theta=wl.rope_theta)
