@@ -103,13 +103,14 @@ struct Staging {
 // current step, built on the host and uploaded once, then reused by every layer with the same
 // configuration.
 struct PlanKey {
-  int window, mfma, tile_q, wg_per_item;
+  int window, mfma, tile_q, wg_per_item, blocks_per_cu;
   int tokens;                  // rows of q / out in the forward call
   int paged;                   // keys through block tables (else dense k/v rows)
   int block_size, num_blocks;  // arena geometry the tables are checked against
   bool operator==(const PlanKey &o) const {
     return window == o.window && mfma == o.mfma && tile_q == o.tile_q &&
-           wg_per_item == o.wg_per_item && tokens == o.tokens && paged == o.paged &&
+           wg_per_item == o.wg_per_item && blocks_per_cu == o.blocks_per_cu &&
+           tokens == o.tokens && paged == o.paged &&
            block_size == o.block_size && num_blocks == o.num_blocks;
   }
 };
@@ -118,8 +119,9 @@ struct Plan {
   PlanKey key{};
   bool valid = false;
   int num_rows = 0, num_merge = 0, num_tiles = 0, num_parts = 0;
+  int num_slots = 0;  // prefill stream-K slots (grid x)
   bool covers_all = true;  // every output row is written by some kernel
-  size_t off_rows = 0, off_merge = 0, off_tiles = 0;
+  size_t off_rows = 0, off_merge = 0, off_tiles = 0, off_slots = 0;
   DevBuf dev;
   Staging stage;
 };
@@ -383,58 +385,68 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   }
   plan->covers_all = covered == key.tokens;
 
-  // Split the key range of long prefill tiles so that no workgroup's serial chain of key tiles
-  // is longer than a quarter of a CU's average share (one 8-wave workgroup runs per CU; with
-  // the longest chunks dispatched first, the makespan is then within ~25% of the ideal).  On
-  // the Qwen3-0.6B varlen prefill, splitting to 1/1, 1/2, 1/4 and 1/8 of the share measured
-  // 0.561, 0.350, 0.310 and 0.320 ms for the kernel.  The chunks of a
-  // tile write partials (query-major, chunk-minor) that the merge kernel combines.
+  // Stream-K schedule of the MFMA tiles.  The grid has exactly as many workgroups per head
+  // group ("slots") as can be resident at once; the 32-key tiles of all query tiles, laid end
+  // to end, are cut into equal runs, one per slot, so every slot finishes at the same time.  A
+  // query tile whose keys fall into several runs becomes several segments; they write partials
+  // (query-major, segment-minor) that the merge kernel combines.  A segment also never spans
+  // more pages than the kernel's LDS copy of the block table holds.
   std::vector<MergeItem> merges;
+  std::vector<int32_t> seg_off;
   int parts = 0;
+  int slots = 0;
   if (!tiles.empty()) {
-    int64_t keys = 0;
-    for (const TileItem &t : tiles) keys += t.ke - t.ks;
-    const int64_t slots = (int64_t)ctx->num_cus * 4;
-    const int64_t share = (keys * key.wg_per_item + slots - 1) / slots;
-    int target = (int)std::max<int64_t>(256, ((share + 31) / 32) * 32);
-    if (paged) {
-      // A chunk's pages must fit the kernel's LDS copy of the block table.
-      const int64_t cap = (int64_t)(kPrefillTablePages - 2) * key.block_size / 32 * 32;
-      target = (int)std::max<int64_t>(32, std::min<int64_t>(target, cap));
-    }
-    std::vector<TileItem> split;
-    split.reserve(tiles.size() * 2);
+    constexpr int KT = 32;
+    int64_t total = 0;
+    for (const TileItem &t : tiles) total += (t.ke - t.ks + KT - 1) / KT;
+    const int64_t resident = (int64_t)ctx->num_cus * key.blocks_per_cu;
+    slots = (int)std::max<int64_t>(1, std::min<int64_t>(total, resident / key.wg_per_item));
+    const int64_t page_cap =
+        paged ? (int64_t)(kPrefillTablePages - 2) * key.block_size / KT * KT : INT32_MAX;
+    std::vector<std::vector<TileItem>> per_slot(slots);
+    int64_t pos = 0;  // first key tile of the current query tile in the flattened order
     for (const TileItem &t : tiles) {
-      const int len = t.ke - t.ks;
-      const bool fits = !paged || (t.ke - 1) / key.block_size - t.ks / key.block_size + 1 <=
-                                      kPrefillTablePages;
-      if (fits && len <= target + target / 4) {
-        split.push_back(t);
-        continue;
+      const int64_t n = (t.ke - t.ks + KT - 1) / KT;
+      // Pieces: cut at slot boundaries (slot s owns [s*total/slots, (s+1)*total/slots)) and at
+      // the page cap.
+      std::vector<std::pair<int, std::pair<int, int>>> pieces;  // slot, [ks, ke)
+      int64_t j = 0;
+      while (j < n) {
+        const int64_t g = pos + j;
+        const int s_of = (int)std::min<int64_t>(slots - 1, g * slots / total);
+        const int64_t s_end = ((int64_t)(s_of + 1) * total + slots - 1) / slots;  // exclusive
+        int64_t take = std::min<int64_t>(n - j, s_end - g);
+        take = std::max<int64_t>(1, std::min<int64_t>(take, page_cap / KT));
+        const int k0 = t.ks + (int)(j * KT);
+        const int k1 = std::min<int>(t.ke, t.ks + (int)((j + take) * KT));
+        pieces.push_back({s_of, {k0, k1}});
+        j += take;
       }
-      const int n = (len + target - 1) / target;
-      const int step = ((len + n - 1) / n + 31) / 32 * 32;
+      pos += n;
+      const int np = (int)pieces.size();
       const int rows = std::min(key.tile_q, t.qlen - t.q0);
-      int made = 0;
-      for (int k0 = t.ks; k0 < t.ke; k0 += step) made++;
-      for (int j = 0; j < made; j++) {
+      for (int pi = 0; pi < np; pi++) {
         TileItem c = t;
-        c.ks = t.ks + j * step;
-        c.ke = std::min(t.ke, c.ks + step);
-        c.part = parts;
-        c.nsplit = made;
-        c.split = j;
-        split.push_back(c);
+        c.ks = pieces[pi].second.first;
+        c.ke = pieces[pi].second.second;
+        c.part = np > 1 ? parts : -1;
+        c.nsplit = np;
+        c.split = pi;
+        per_slot[pieces[pi].first].push_back(c);
       }
-      for (int r = 0; r < rows; r++) merges.push_back({t.qstart + t.q0 + r, parts + r * made, made, 0});
-      parts += rows * made;
+      if (np > 1) {
+        for (int r = 0; r < rows; r++) merges.push_back({t.qstart + t.q0 + r, parts + r * np, np, 0});
+        parts += rows * np;
+      }
     }
-    tiles.swap(split);
+    tiles.clear();
+    seg_off.reserve(slots + 1);
+    for (int sl = 0; sl < slots; sl++) {
+      seg_off.push_back((int32_t)tiles.size());
+      tiles.insert(tiles.end(), per_slot[sl].begin(), per_slot[sl].end());
+    }
+    seg_off.push_back((int32_t)tiles.size());
   }
-  // Longest tiles first: the grid is dispatched roughly in order, so this is an LPT schedule.
-  std::stable_sort(tiles.begin(), tiles.end(), [](const TileItem &a, const TileItem &b) {
-    return (a.ke - a.ks) > (b.ke - b.ks);
-  });
 
   // Chunk: the largest of 1024..64 keys that still gives the grid >= 8 workgroups per CU.
   int64_t total = 0;
@@ -480,10 +492,12 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   plan->num_merge = (int)merges.size();
   plan->num_tiles = (int)tiles.size();
   plan->num_parts = parts;
+  plan->num_slots = slots;
   plan->off_rows = 0;
   plan->off_merge = plan->off_rows + items.size() * sizeof(RowItem);
   plan->off_tiles = plan->off_merge + merges.size() * sizeof(MergeItem);
-  const size_t bytes = plan->off_tiles + tiles.size() * sizeof(TileItem);
+  plan->off_slots = plan->off_tiles + tiles.size() * sizeof(TileItem);
+  const size_t bytes = plan->off_slots + seg_off.size() * sizeof(int32_t);
   if (bytes > 0) {
     HIP_TRY(ctx, plan->stage.reserve(bytes), "plan staging");
     HIP_TRY(ctx, plan->dev.reserve(bytes), "plan buffer");
@@ -492,6 +506,8 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     if (!merges.empty())
       memcpy(h + plan->off_merge, merges.data(), merges.size() * sizeof(MergeItem));
     if (!tiles.empty()) memcpy(h + plan->off_tiles, tiles.data(), tiles.size() * sizeof(TileItem));
+    if (!seg_off.empty())
+      memcpy(h + plan->off_slots, seg_off.data(), seg_off.size() * sizeof(int32_t));
     HIP_TRY(ctx, plan->stage.upload(plan->dev, bytes, ctx->stream), "plan upload");
   }
   plan->valid = true;
@@ -538,6 +554,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   key.mfma = mfma ? 1 : 0;
   key.tile_q = mfma ? prefill_tile_queries(hpw_tile) : 0;
   key.wg_per_item = d.num_kv_heads * (rep / hpw_row);
+  key.blocks_per_cu = mfma ? prefill_blocks_per_cu(d.head_dim, hpw_tile) : 0;
   key.tokens = num_tokens;
   key.paged = view.paged;
   key.block_size = view.paged ? view.block_size : 0;
@@ -565,7 +582,9 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     t.out = out;
     t.kv = view;
     t.items = reinterpret_cast<const TileItem *>(pbase + plan->off_tiles);
+    t.seg_off = reinterpret_cast<const int32_t *>(pbase + plan->off_slots);
     t.num_items = plan->num_tiles;
+    t.num_slots = plan->num_slots;
     t.hq = d.num_heads;
     t.hkv = d.num_kv_heads;
     t.head_dim = d.head_dim;

@@ -30,8 +30,11 @@ struct MergeItem {
   int32_t pad;
 };
 
-// One workgroup of the MFMA prefill kernel: a tile of queries of one sequence, for one KV
-// head (and a group of its query heads), over the key tiles [ks, ke).
+// One segment of the MFMA prefill kernel: a tile of queries of one sequence, for one KV head
+// (and a group of its query heads), over the keys [ks, ke).  A workgroup runs the segments of
+// its slot one after another (a stream-K schedule: every slot gets the same number of key
+// tiles, so a query tile whose keys straddle two slots becomes two segments whose partials are
+// merged).
 struct TileItem {
   int32_t seq;     // block-table row (paged) / sequence index
   int32_t qstart;  // row of the sequence's first query in q/out
@@ -80,8 +83,10 @@ struct TileLaunch {
   const float *q;
   float *out;
   KvView kv;
-  const TileItem *items;
+  const TileItem *items;     // segments, grouped by slot
+  const int32_t *seg_off;    // [num_slots + 1]: slot s runs items [seg_off[s], seg_off[s+1])
   int32_t num_items;
+  int32_t num_slots;         // workgroups along x (each runs its slot's segments in order)
   int32_t hq, hkv, head_dim;
   int32_t window;  // 0 = none
   float scale;
@@ -138,6 +143,8 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream
 // Shapes the kernels are instantiated for.
 bool row_kernel_supports(int head_dim, int heads_per_wg);
 bool prefill_kernel_supports(int head_dim, int heads_per_wg);
+// Prefill workgroups that can be resident on one CU at once (occupancy of the kernel).
+int prefill_blocks_per_cu(int head_dim, int heads_per_wg);
 
 // Most pages one prefill key chunk may span (its block ids are staged in LDS).
 constexpr int kPrefillTablePages = 128;

@@ -7,23 +7,28 @@
 // Keys come from dense k/v rows (prefillDense) or from the cache through the block table
 // (prefillWithCache).
 //
-// Mapping onto CDNA4.  A workgroup (4 waves) owns a tile of queries of one sequence for one KV
-// head and HPW of its query heads, over one chunk [ks, ke) of the keys (long key ranges are
-// split across workgroups and merged afterwards, so no workgroup's serial chain is much longer
-// than the average).  Wave w handles 32 queries of one head.
+// Mapping onto CDNA4.  The grid is exactly as many workgroups per head group as can be
+// resident at once; each runs the segments of its slot of a stream-K schedule (equal numbers
+// of 32-key tiles per slot; a query tile whose keys straddle slots is split and its partials
+// merged).  The whole step's K/V (tens of MB) stays in the 256 MB Infinity Cache, which all
+// XCDs share, so slots need no XCD-aware placement.  A segment is a tile of 16 * 8 / HPW queries of one
+// sequence for HPW query heads of one KV head, over a key range [ks, ke).  The 8 waves of the
+// workgroup each own 16 queries of one head.
 //   * Key tiles of 32 rows of K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
 //     register staging), double-buffered so the next tile streams in while this one is used;
 //     one barrier per tile.  Rows are stored unpadded; K rows have their 16-byte chunks
-//     XOR-swizzled by (row & 7) so the column reads of QK are conflict-free, V rows are read
-//     along the row and need no swizzle.
+//     XOR-swizzled by (row & 15) so the column reads of QK are conflict-free, V rows are read
+//     along the row and need no swizzle.  The block ids of the segment's pages are staged in LDS
+//     once, so a paged tile load never waits on a global table read.
 //   * Per tile each wave computes (D = 128)
-//       S^T[key][query] = K Q^T      64 x v_mfma_f32_32x32x2_f32, K from LDS (ds_read_b128),
-//                                    Q (32 x D/2 per lane) resident in registers;
-//       O^T[dim][query] += V^T P^T   64 x v_mfma_f32_32x32x2_f32, one ds_read_b128 of V feeds
-//                                    4 MFMAs (output block b holds dims 4r + b).
-//     With S transposed each lane holds 16 keys of ONE query: the row max is an in-lane max plus
-//     one exchange with lane^32, and P^T lands exactly in the registers the PV MFMA reads as its
-//     B operand (the key order of the contraction is permuted to match), so P never touches LDS.
+//       S^T[key][query] = K Q^T      64 x v_mfma_f32_16x16x4_f32, K from LDS (ds_read_b128),
+//                                    Q (16 queries x D/4 per lane) resident in registers;
+//       O^T[dim][query] += V^T P^T   64 x v_mfma_f32_16x16x4_f32, one ds_read_b128 of V feeds
+//                                    4 MFMAs (output block 4*hh + b holds dims 64*hh + 4r + b).
+//     With S transposed each lane holds 8 keys of ONE query: the row max is an in-lane max plus
+//     exchanges with lane^16 and lane^32, and P^T lands exactly in the registers the PV MFMA
+//     reads as its B operand (the key order of the contraction is permuted to match), so P
+//     never touches LDS.
 //   * Softmax runs in the log2 domain (scale * log2 e folded into the score, v_exp_f32), and the
 //     running max is only moved -- and O rescaled -- when a tile's max exceeds it by more than
 //     2^8, which after the first tiles almost never happens.
@@ -86,7 +91,12 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
   __shared__ __attribute__((aligned(16))) float sv1[TILE];
   __shared__ int32_t stab[kTablePages];  // block ids of the pages this chunk touches
 
-  const TileItem it = a.items[blockIdx.x];
+  const int slot = blockIdx.x;
+  const int seg_end = a.seg_off[slot + 1];
+  for (int seg = a.seg_off[slot]; seg < seg_end; seg++) {
+  // Every wave is done with the previous segment's LDS tiles and table before they are reused.
+  __syncthreads();
+  const TileItem it = a.items[seg];
   const int rep = a.hq / a.hkv;
   const int groups = rep / HPW;
   const int kvh = blockIdx.y / groups;
@@ -265,7 +275,7 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
 
   float l_tot = l_run + __shfl_xor(l_run, 16);
   l_tot += __shfl_xor(l_tot, 32);
-  if (!qvalid || !wave_active) return;
+  if (!qvalid || !wave_active) continue;
   // Lane (i, g) holds O^T rows r = 4g + v of every block: dims 64*hh + 4r + bb.
   float *op;
   float inv = 1.0f;
@@ -291,13 +301,14 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
     a.part_m[pidx] = m_run;
     a.part_l[pidx] = l_tot;
   }
+  }  // segments
 }
 
 namespace {
 
 template <int D>
 hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
-  const dim3 grid(a.num_items, a.hkv * ((a.hq / a.hkv) / hpw));
+  const dim3 grid(a.num_slots, a.hkv * ((a.hq / a.hkv) / hpw));
   switch (hpw) {
     case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(512), 0, s, a); break;
     case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(512), 0, s, a); break;
@@ -315,8 +326,40 @@ bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
          (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8);
 }
 
+namespace {
+
+template <int D, int HPW>
+int blocks_per_cu() {
+  static int n = -1;
+  if (n < 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, prefill_kernel<D, HPW>, 512, 0) !=
+            hipSuccess ||
+        b < 1)
+      b = 1;
+    n = b;
+  }
+  return n;
+}
+
+template <int D>
+int blocks_per_cu_d(int hpw) {
+  switch (hpw) {
+    case 1: return blocks_per_cu<D, 1>();
+    case 2: return blocks_per_cu<D, 2>();
+    case 4: return blocks_per_cu<D, 4>();
+    default: return blocks_per_cu<D, 8>();
+  }
+}
+
+}  // namespace
+
+int prefill_blocks_per_cu(int head_dim, int heads_per_wg) {
+  return head_dim == 64 ? blocks_per_cu_d<64>(heads_per_wg) : blocks_per_cu_d<128>(heads_per_wg);
+}
+
 hipError_t launch_prefill_tiles(const TileLaunch &a, int hpw, hipStream_t s) {
-  if (a.num_items <= 0) return hipSuccess;
+  if (a.num_items <= 0 || a.num_slots <= 0) return hipSuccess;
   switch (a.head_dim) {
     case 64: return launch_prefill_d<64>(a, hpw, s);
     case 128: return launch_prefill_d<128>(a, hpw, s);
