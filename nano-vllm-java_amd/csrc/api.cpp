@@ -737,7 +737,6 @@ nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &
                        num_tokens, out);
 }
 
-// Math.round(float), Norms.java:317: floor(x + 1/2) evaluated exactly; NaN -> 0; saturating.
 // The kernels' view of an RMSNorm descriptor; NULL disables the norm.  Any eps is accepted, as
 // in the reference (a negative var + eps gives NaN there too).
 HeadNorm head_norm(const nva_rms_norm *n) {
@@ -751,6 +750,7 @@ HeadNorm head_norm(const nva_rms_norm *n) {
   return h;
 }
 
+// Math.round(float), Norms.java:317: floor(x + 1/2) evaluated exactly; NaN -> 0; saturating.
 int32_t java_round(float x) {
   if (std::isnan(x)) return 0;
   const float f = std::floor(x);

@@ -1,0 +1,184 @@
+"""Parity of the shared-KV branch and per-layer head dims on the GPU, through the C ABI.
+
+A layer with writeKv = false reads the pages of its producer layer (kvLayerIndex) and writes
+nothing (Attention.attendFromCache, layers/Attention.java:176-216): decode and paged prefill
+read the pages through the block tables; dense prefill gathers the producer's rows at the
+step's slots (gatherKvCache) and runs the dense path over them; with neither tables nor slots
+the call fails like the reference's IllegalStateException.  The arena mixes head dims and has
+an unallocated layer (KvCacheArena(numBlocks, blockSize, Hkv, headDims[], allocate[]),
+engine/KvCacheArena.java:63-90).  Bar: outputs within max-abs 1e-4 / rel-L2 1e-5 of the
+oracle; every page byte of every layer unchanged."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from cases import rel_l2
+from nanollvm_amd import (Attention, Context, IllegalStateException, KvCacheArena, RMSNorm,
+                          RotaryEmbedding)
+from nanollvm_amd import workloads as W
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, BS = 4, 2, 16
+DIMS = [32, 16, 32]          # layer 2 is a shared layer: it owns no pages
+ALLOC = [True, True, False]
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def make_arena(ctx, wl, rng):
+    arena = KvCacheArena(ctx, len(DIMS), wl.num_blocks, BS, HKV, head_dims=DIMS,
+                         allocate=ALLOC)
+    pages = {}
+    for layer, d in enumerate(DIMS):
+        if not ALLOC[layer]:
+            continue
+        shape = (wl.num_blocks, BS, HKV, d)
+        kc = rng.standard_normal(shape).astype(np.float32)
+        vc = rng.standard_normal(shape).astype(np.float32)
+        arena.write(layer, 0, kc)
+        arena.write(layer, 1, vc)
+        pages[layer] = (kc, vc)
+    return arena, pages
+
+
+def check_pages_unchanged(arena, pages):
+    for layer, (kc, vc) in pages.items():
+        assert np.array_equal(bits(arena.get_key_cache(layer)), bits(kc)), f"K layer {layer}"
+        assert np.array_equal(bits(arena.get_value_cache(layer)), bits(vc)), f"V layer {layer}"
+    _, _, nbytes = arena.device_ptrs(2)
+    assert nbytes == 0
+
+
+def run_shared(ctx, wl, name, drop_tables=False, window=0):
+    say(f"{name}: tokens={wl.tokens} d=32 producer=0 window={window}")
+    rng = np.random.default_rng(9)
+    arena, pages = make_arena(ctx, wl, rng)
+    try:
+        m = wl.meta
+        args = m.context_args()
+        if drop_tables:
+            args["block_tables"] = None
+        ctx.set(**args)
+        ctx.bind_kv_cache(arena)
+        q = rng.standard_normal((wl.tokens, HQ, 32)).astype(np.float32)
+        attn = Attention(HQ, 32, 0.2, HKV, window, kv_layer_index=0, write_kv=False)
+        out = attn.forward(dev(q), None, None, ctx)
+        ctx.sync()
+        kc, vc = pages[0]
+        want = O.attention_forward(HQ, 32, 0.2, HKV, is_prefill=m.is_prefill, q=q,
+                                   cu_q=m.cu_seqlens_q, cu_k=m.cu_seqlens_k,
+                                   slot_mapping=m.slot_mapping, context_lens=m.context_lens,
+                                   block_tables=None if drop_tables else m.block_tables,
+                                   k_cache=kc.copy(), v_cache=vc.copy(), sliding_window=window,
+                                   write_kv=False, threads=4)
+        got = out.cpu().numpy()
+        err = float(np.max(np.abs(got - want)))
+        rl2 = rel_l2(got, want)
+        say(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+        assert err <= 1e-4 and rl2 <= 1e-5
+        check_pages_unchanged(arena, pages)
+    finally:
+        ctx.clear()
+        arena.close()
+
+
+def test_shared_decode(ctx):
+    wl = W.build("shared decode", [(c - 1, 1) for c in (1, 16, 17, 90, 200)], is_prefill=False,
+                 hq=HQ, hkv=HKV, d=32, scale=0.2, rng=np.random.default_rng(1), block_size=BS)
+    run_shared(ctx, wl, "shared decode")
+    run_shared(ctx, wl, "shared decode window 7", window=7)
+
+
+def test_shared_paged_prefill(ctx):
+    wl = W.build("shared prefill", [(16, 40), (0, 70), (5, 1), (33, 12)], is_prefill=True,
+                 hq=HQ, hkv=HKV, d=32, scale=0.2, rng=np.random.default_rng(2), block_size=BS)
+    run_shared(ctx, wl, "shared paged prefill")
+
+
+def test_shared_dense_prefill_gathers(ctx):
+    wl = W.build("shared dense", [(0, 40), (0, 70), (0, 3)], is_prefill=True, hq=HQ, hkv=HKV,
+                 d=32, scale=0.2, rng=np.random.default_rng(3), block_size=BS)
+    run_shared(ctx, wl, "shared dense prefill (gather)", drop_tables=True)
+
+
+def test_shared_dense_prefill_without_slots_fails(ctx):
+    wl = W.build("shared dense", [(0, 10)], is_prefill=True, hq=HQ, hkv=HKV, d=32, scale=0.2,
+                 rng=np.random.default_rng(4), block_size=BS)
+    arena, pages = make_arena(ctx, wl, np.random.default_rng(5))
+    try:
+        args = wl.meta.context_args()
+        args["block_tables"] = None
+        args["slot_mapping"] = None
+        ctx.set(**args)
+        ctx.bind_kv_cache(arena)
+        q = torch.zeros((wl.tokens, HQ, 32), device="cuda")
+        with pytest.raises(IllegalStateException):
+            Attention(HQ, 32, 0.2, HKV, 0, kv_layer_index=0, write_kv=False).forward(
+                q, None, None, ctx)
+        check_pages_unchanged(arena, pages)
+    finally:
+        ctx.clear()
+        arena.close()
+
+
+def test_gemma4_shared_layer_fused_norm_rope(ctx):
+    """Gemma4Attention.forward on a shared layer (Gemma4ForCausalLM.java:164-176): q is
+    normalised and rotated, k/v are zeros that are neither stored nor read; attention reads the
+    producer's pages."""
+    wl = W.build("gemma4 shared", [(c - 1, 1) for c in (3, 50, 129)], is_prefill=False, hq=HQ,
+                 hkv=HKV, d=32, scale=1.0, rng=np.random.default_rng(6), block_size=BS)
+    say("gemma4 shared layer: fused q norm + rope, write_kv=0")
+    rng = np.random.default_rng(10)
+    arena, pages = make_arena(ctx, wl, rng)
+    table = O.rope_table(32, 512, 1e6)
+    rope = RotaryEmbedding(ctx, 32, 32, 512, 1e6, cos_sin=table)
+    try:
+        m = wl.meta
+        ctx.set(**m.context_args())
+        ctx.bind_kv_cache(arena)
+        q = rng.standard_normal((wl.tokens, HQ, 32)).astype(np.float32)
+        zeros = np.zeros((wl.tokens, HKV, 32), np.float32)
+        qw = rng.standard_normal(32).astype(np.float32)
+        q_out = torch.empty((wl.tokens, HQ, 32), device="cuda")
+        attn = Attention(HQ, 32, 1.0, HKV, 0, kv_layer_index=0, write_kv=False)
+        out = attn.forward_with_norm_rope(rope, m.positions, dev(q), dev(zeros), dev(zeros), ctx,
+                                          q_norm=RMSNorm(dev(qw), 1e-6), q_out=q_out)
+        nq = O.rms_norm(q.reshape(-1, 32), qw, 1e-6).reshape(q.shape)
+        qr, _ = O.rope_forward(table, m.positions, nq, zeros)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(q_out.cpu().numpy()), bits(qr))
+        kc, vc = pages[0]
+        want = O.attention_forward(HQ, 32, 1.0, HKV, is_prefill=False, q=qr,
+                                   slot_mapping=m.slot_mapping, context_lens=m.context_lens,
+                                   block_tables=m.block_tables, k_cache=kc.copy(),
+                                   v_cache=vc.copy(), write_kv=False)
+        got = out.cpu().numpy()
+        assert np.max(np.abs(got - want)) <= 1e-4 and rel_l2(got, want) <= 1e-5
+        check_pages_unchanged(arena, pages)
+    finally:
+        ctx.clear()
+        arena.close()
+        rope.close()
