@@ -543,7 +543,7 @@ KvView make_dense_view(const float *k, const float *v) {
 nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &view,
                          int num_blocks, const float *q, int num_tokens, float *out) {
   const int rep = d.num_heads / d.num_kv_heads;
-  const int hpw_row = largest_pow2_divisor_upto(rep, 8);
+  const int hpw_row = largest_pow2_divisor_upto(rep, row_kernel_max_heads(d.head_dim));
   const int hpw_tile = largest_pow2_divisor_upto(rep, 8);
   const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, hpw_tile);
   if (!row_kernel_supports(d.head_dim, hpw_row))

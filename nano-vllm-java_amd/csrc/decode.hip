@@ -14,9 +14,10 @@
 //   * one workgroup (4 waves) per (work item, KV head, group of HPW query heads); a work item
 //     is one query row and a chunk of its key range (the host splits long rows so that every
 //     workgroup reads about the same number of bytes and the grid has thousands of groups);
-//   * a K/V row (D fp32) is read by LPT = D/4 lanes as float4: each wave load instruction
-//     fetches TPW = 64/LPT whole rows, i.e. contiguous 128-byte lines, and all HPW query heads
-//     of the KV head reuse the registers (K/V are read from HBM exactly once per KV head);
+//   * a K/V row (D fp32) is read by LPT = min(64, D/4) lanes, VPL = D/(4*LPT) float4 each
+//     (VPL = 2 at D = 512): each wave load instruction fetches TPW = 64/LPT whole rows, i.e.
+//     contiguous 128-byte lines, and all HPW query heads of the KV head reuse the registers
+//     (K/V are read from HBM exactly once per KV head);
 //   * the dot products are reduced across the LPT lanes with DPP row ops and one swizzle (no
 //     LDS traffic); each group of LPT lanes is an independent online-softmax stream;
 //   * the 4*TPW streams of the workgroup are merged through LDS at the end, and either the
@@ -71,14 +72,15 @@ __device__ __forceinline__ int64_t kv_row(const KvView &kv, const int32_t *table
 
 template <int D, int HPW>
 __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
-  constexpr int LPT = D / 4;        // lanes per K/V row
-  constexpr int TPW = 64 / LPT;     // rows per wave load instruction
-  constexpr int U = 8;              // rows per stream per group
-  constexpr int G = TPW * U;        // rows per wave per group
-  constexpr int NS = 4 * TPW;       // softmax streams per workgroup
+  constexpr int LPT = D / 4 < 64 ? D / 4 : 64;  // lanes per K/V row
+  constexpr int VPL = D / (4 * LPT);            // float4 per lane per row
+  constexpr int TPW = 64 / LPT;                 // rows per wave load instruction
+  constexpr int U = 8 / VPL;                    // rows per stream per group
+  constexpr int G = TPW * U;                    // rows per wave per group
+  constexpr int NS = 4 * TPW;                   // softmax streams per workgroup
   __shared__ float sm_m[NS][HPW];
   __shared__ float sm_l[NS][HPW];
-  __shared__ float4 sm_acc[NS][HPW][LPT];
+  __shared__ float4 sm_acc[NS][HPW][LPT * VPL];
 
   const RowItem it = a.items[blockIdx.x];
   const int rep = a.hq / a.hkv;
@@ -90,9 +92,13 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   const int sub = lane / LPT;
   const int c = lane - sub * LPT;
 
-  float4 qv[HPW];
+  // Lane c holds dims [4c + 4*LPT*j, +4) for j < VPL, so each load instruction is contiguous.
+  float4 qv[HPW][VPL];
 #pragma unroll
-  for (int h = 0; h < HPW; h++) qv[h] = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + c * 4);
+  for (int h = 0; h < HPW; h++)
+#pragma unroll
+    for (int j = 0; j < VPL; j++)
+      qv[h][j] = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + (c + LPT * j) * 4);
   const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
 
   const size_t rs = (size_t)a.hkv * D;
@@ -101,34 +107,45 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   const int32_t *table = a.kv.paged ? a.kv.table + (size_t)it.seq * a.kv.bt_stride : nullptr;
 
   float m[HPW], l[HPW];
-  float4 acc[HPW];
+  float4 acc[HPW][VPL];
 #pragma unroll
   for (int h = 0; h < HPW; h++) {
     m[h] = -INFINITY;
     l[h] = 0.0f;
-    acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < VPL; j++) acc[h][j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
   for (int g0 = it.kbeg + wave * G; g0 < it.kend; g0 += 4 * G) {
-    float4 kr[U], vr[U];
+    float4 kr[U][VPL], vr[U][VPL];
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int t = g0 + u * TPW + sub;
       ok[u] = t < it.kend;
       const int64_t row = kv_row(a.kv, table, it.kbase, ok[u] ? t : it.kbeg);
-      kr[u] = ld4(kp + row * rs);
-      vr[u] = ld4(vp + row * rs);
+#pragma unroll
+      for (int j = 0; j < VPL; j++) {
+        kr[u][j] = ld4(kp + row * rs + LPT * 4 * j);
+        vr[u][j] = ld4(vp + row * rs + LPT * 4 * j);
+      }
     }
 #pragma unroll
     for (int h = 0; h < HPW; h++) {
       float s[U];
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        float p = qv[h].x * kr[u].x;
-        p = fmaf(qv[h].y, kr[u].y, p);
-        p = fmaf(qv[h].z, kr[u].z, p);
-        p = fmaf(qv[h].w, kr[u].w, p);
+        float p = qv[h][0].x * kr[u][0].x;
+        p = fmaf(qv[h][0].y, kr[u][0].y, p);
+        p = fmaf(qv[h][0].z, kr[u][0].z, p);
+        p = fmaf(qv[h][0].w, kr[u][0].w, p);
+#pragma unroll
+        for (int j = 1; j < VPL; j++) {
+          p = fmaf(qv[h][j].x, kr[u][j].x, p);
+          p = fmaf(qv[h][j].y, kr[u][j].y, p);
+          p = fmaf(qv[h][j].z, kr[u][j].z, p);
+          p = fmaf(qv[h][j].w, kr[u][j].w, p);
+        }
         s[u] = group_sum<LPT>(p);
       }
       float mx = -INFINITY;
@@ -141,21 +158,29 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       const float ms = mn == -INFINITY ? 0.0f : mn;
       const float alpha = __builtin_amdgcn_exp2f(m[h] - ms);
       float ls = 0.0f;
-      float4 av = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 av[VPL];
+#pragma unroll
+      for (int j = 0; j < VPL; j++) av[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const float w = __builtin_amdgcn_exp2f(s[u] - ms);
         ls += w;
-        av.x = fmaf(w, vr[u].x, av.x);
-        av.y = fmaf(w, vr[u].y, av.y);
-        av.z = fmaf(w, vr[u].z, av.z);
-        av.w = fmaf(w, vr[u].w, av.w);
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+          av[j].x = fmaf(w, vr[u][j].x, av[j].x);
+          av[j].y = fmaf(w, vr[u][j].y, av[j].y);
+          av[j].z = fmaf(w, vr[u][j].z, av[j].z);
+          av[j].w = fmaf(w, vr[u][j].w, av[j].w);
+        }
       }
       l[h] = fmaf(l[h], alpha, ls);
-      acc[h].x = fmaf(acc[h].x, alpha, av.x);
-      acc[h].y = fmaf(acc[h].y, alpha, av.y);
-      acc[h].z = fmaf(acc[h].z, alpha, av.z);
-      acc[h].w = fmaf(acc[h].w, alpha, av.w);
+#pragma unroll
+      for (int j = 0; j < VPL; j++) {
+        acc[h][j].x = fmaf(acc[h][j].x, alpha, av[j].x);
+        acc[h][j].y = fmaf(acc[h][j].y, alpha, av[j].y);
+        acc[h][j].z = fmaf(acc[h][j].z, alpha, av[j].z);
+        acc[h][j].w = fmaf(acc[h][j].w, alpha, av[j].w);
+      }
       m[h] = mn;
     }
   }
@@ -167,13 +192,15 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       sm_m[stream][h] = m[h];
       sm_l[stream][h] = l[h];
     }
-    sm_acc[stream][h][c] = acc[h];
+#pragma unroll
+    for (int j = 0; j < VPL; j++) sm_acc[stream][h][c + LPT * j] = acc[h][j];
   }
   __syncthreads();
 
-  for (int idx = threadIdx.x; idx < HPW * LPT; idx += blockDim.x) {
-    const int h = idx / LPT;
-    const int cc = idx - h * LPT;
+  // sm_acc[.][h][cc] holds dims [4cc, 4cc + 4) of head h.
+  for (int idx = threadIdx.x; idx < HPW * LPT * VPL; idx += blockDim.x) {
+    const int h = idx / (LPT * VPL);
+    const int cc = idx - h * (LPT * VPL);
     float M = -INFINITY;
     for (int s = 0; s < NS; s++) M = fmaxf(M, sm_m[s][h]);
     const float Ms = M == -INFINITY ? 0.0f : M;
@@ -243,7 +270,12 @@ hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
     case 1: hipLaunchKernelGGL((row_attention_kernel<D, 1>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((row_attention_kernel<D, 2>), grid, dim3(256), 0, s, a); break;
     case 4: hipLaunchKernelGGL((row_attention_kernel<D, 4>), grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((row_attention_kernel<D, 8>), grid, dim3(256), 0, s, a); break;
+    case 8:
+      if constexpr (D <= 256) {
+        hipLaunchKernelGGL((row_attention_kernel<D, 8>), grid, dim3(256), 0, s, a);
+        break;
+      }
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -253,11 +285,13 @@ hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
 
 bool row_kernel_supports(int head_dim, int heads_per_wg) {
   const bool d_ok = head_dim == 4 || head_dim == 8 || head_dim == 16 || head_dim == 32 ||
-                    head_dim == 64 || head_dim == 128 || head_dim == 256;
+                    head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512;
   const bool h_ok = heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 ||
-                    heads_per_wg == 8;
+                    (heads_per_wg == 8 && head_dim <= 256);
   return d_ok && h_ok;
 }
+
+int row_kernel_max_heads(int head_dim) { return head_dim <= 256 ? 8 : 4; }
 
 hipError_t launch_row_attention(const RowLaunch &a, int hpw, hipStream_t s) {
   if (a.num_items <= 0) return hipSuccess;
@@ -269,6 +303,7 @@ hipError_t launch_row_attention(const RowLaunch &a, int hpw, hipStream_t s) {
     case 64: return launch_row_d<64>(a, hpw, s);
     case 128: return launch_row_d<128>(a, hpw, s);
     case 256: return launch_row_d<256>(a, hpw, s);
+    case 512: return launch_row_d<512>(a, hpw, s);
     default: return hipErrorInvalidValue;
   }
 }

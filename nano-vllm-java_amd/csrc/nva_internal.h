@@ -142,6 +142,8 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream
 
 // Shapes the kernels are instantiated for.
 bool row_kernel_supports(int head_dim, int heads_per_wg);
+// Most query heads one row-kernel workgroup carries at this head dim (register budget).
+int row_kernel_max_heads(int head_dim);
 bool prefill_kernel_supports(int head_dim, int heads_per_wg);
 // Prefill workgroups that can be resident on one CU at once (occupancy of the kernel).
 int prefill_blocks_per_cu(int head_dim, int heads_per_wg);

@@ -182,3 +182,65 @@ def test_gemma4_shared_layer_fused_norm_rope(ctx):
         ctx.clear()
         arena.close()
         rope.close()
+
+
+@pytest.mark.parametrize("is_prefill", [False, True])
+def test_gemma4_like_arena_mixed_head_dims(ctx, is_prefill):
+    """A Gemma-4-shaped stack (Config.headDimForLayer / kvLayerIndexForLayer,
+    llm/Config.java:805-883): sliding layers d = 256 with a 512-token window, global layers
+    d = 512, 8 q heads / 1 kv head; layers 2 and 3 are shared consumers of layers 0 and 1.  One
+    step runs every layer; producers store, consumers read the producer's pages."""
+    dims, alloc, producer, window = [256, 512, 256, 512], [1, 1, 0, 0], [0, 1, 0, 1], [512, 0,
+                                                                                     512, 0]
+    hq, hkv = 8, 1
+    seqs = [(c - 1, 1) for c in (7, 300, 700)] if not is_prefill else [(0, 40), (256, 30)]
+    rng = np.random.default_rng(12)
+    wl = W.build("gemma4 stack", seqs, is_prefill=is_prefill, hq=hq, hkv=hkv, d=256, scale=1.0,
+                 rng=rng, block_size=BS)
+    say(f"gemma4-like stack prefill={is_prefill} dims={dims}")
+    arena = KvCacheArena(ctx, 4, wl.num_blocks, BS, hkv, head_dims=dims,
+                         allocate=[bool(a) for a in alloc])
+    pages = {}
+    for layer in (0, 1):
+        shape = (wl.num_blocks, BS, hkv, dims[layer])
+        kc = np.full(shape, np.nan, np.float32)
+        vc = np.full(shape, np.nan, np.float32)
+        prior = wl.prior_slots()
+        kc.reshape(-1, hkv, dims[layer])[prior] = rng.standard_normal(
+            (len(prior), hkv, dims[layer])).astype(np.float32)
+        vc.reshape(-1, hkv, dims[layer])[prior] = rng.standard_normal(
+            (len(prior), hkv, dims[layer])).astype(np.float32)
+        arena.write(layer, 0, kc)
+        arena.write(layer, 1, vc)
+        pages[layer] = [kc, vc]
+    try:
+        m = wl.meta
+        ctx.set(**m.context_args())
+        ctx.bind_kv_cache(arena)
+        for layer in range(4):
+            d = dims[layer]
+            q = rng.standard_normal((wl.tokens, hq, d)).astype(np.float32)
+            k = rng.standard_normal((wl.tokens, hkv, d)).astype(np.float32)
+            v = rng.standard_normal((wl.tokens, hkv, d)).astype(np.float32)
+            writes = alloc[layer] == 1
+            attn = Attention(hq, d, 1.0, hkv, window[layer], kv_layer_index=producer[layer],
+                             write_kv=writes)
+            out = attn.forward(dev(q), dev(k), dev(v), ctx)
+            kc, vc = pages[producer[layer]]
+            want = O.attention_forward(hq, d, 1.0, hkv, is_prefill=is_prefill, q=q, k=k, v=v,
+                                       cu_q=m.cu_seqlens_q, cu_k=m.cu_seqlens_k,
+                                       slot_mapping=m.slot_mapping, context_lens=m.context_lens,
+                                       block_tables=m.block_tables, k_cache=kc, v_cache=vc,
+                                       sliding_window=window[layer], write_kv=writes, threads=4)
+            got = out.cpu().numpy()
+            err = float(np.max(np.abs(got - want)))
+            rl2 = rel_l2(got, want)
+            say(f"layer {layer} d={d} writes={writes}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+            assert err <= 1e-4 and rl2 <= 1e-5
+        for layer in (0, 1):
+            kc, vc = pages[layer]
+            assert np.array_equal(bits(arena.get_key_cache(layer)), bits(kc))
+            assert np.array_equal(bits(arena.get_value_cache(layer)), bits(vc))
+    finally:
+        ctx.clear()
+        arena.close()
