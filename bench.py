@@ -2,8 +2,9 @@
 """Benchmark of the paged attention path on one MI355X.
 
 One step = one attention layer pass over one scheduler step's batch, with the step metadata
-already uploaded and every input resident in HBM: the fused RoPE + K/V store kernel, then the
-attention kernels (split-KV decode + merge, or MFMA prefill).
+already uploaded and every input resident in HBM: the fused kernel that applies Qwen3's per-head
+q/k RMSNorm, RoPE and the K/V store, then the attention kernels (split-KV decode + merge, or
+MFMA prefill).
 
 Headline (``value``): decode attention at the Qwen3-0.6B shape with 256 sequences of
 log-uniform context in [128, 32768] (fragmented block tables, ~15 GB of K/V resident), in GB/s
@@ -116,6 +117,26 @@ def decode_bytes(wl):
     return kv + qo + 4 * (pages + rows)
 
 
+def head_norms(wl, seed):
+    """Qwen3's per-head q_norm / k_norm (RMSNorm over head_dim, eps 1e-6) with synthetic
+    weights near 1."""
+    import torch
+    from nanollvm_amd import RMSNorm
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    qw = 1.0 + 0.1 * torch.randn(wl.d, device="cuda", generator=g)
+    kw = 1.0 + 0.1 * torch.randn(wl.d, device="cuda", generator=g)
+    return RMSNorm(qw, 1e-6), RMSNorm(kw, 1e-6)
+
+
+def kernel_a_bytes(wl, k_out):
+    """Algorithmic bytes of the fused norm + RoPE + store kernel: q/k/v read, rotated q (and k)
+    written, the rotated k and v rows stored, one cos|sin row, position and slot per token."""
+    T, hq, hkv, d = wl.tokens, wl.hq, wl.hkv, wl.d
+    return T * (4 * d * (hq + 2 * hkv) + 4 * d * (hq + (hkv if k_out else 0)) +
+                4 * d * 2 * hkv + 4 * d + 8)
+
+
 def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, label):
     import torch
     from nanollvm_amd import Context  # noqa: F401
@@ -123,15 +144,21 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
     pos = wl.meta.positions
+    qn, kn = head_norms(wl, 11)
+
+    def step():
+        attn.forward_with_norm_rope(rope, pos, q, k, v, ctx, q_norm=qn, k_norm=kn, q_out=out_q,
+                                    k_out=out_k)
+
     for _ in range(warmup):
-        attn.forward_with_rope(rope, pos, q, k, v, ctx, q_out=out_q, k_out=out_k)
+        step()
     torch.cuda.synchronize()
     ctx.reset_stats()
     ctx.set_timing(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        attn.forward_with_rope(rope, pos, q, k, v, ctx, q_out=out_q, k_out=out_k)
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ctx.set_timing(False)
@@ -141,6 +168,49 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
     log(f"{label}: {ms:.4f} ms/step; kernels " + ", ".join(
         f"{n}={s[1] / max(s[0], 1):.4f}ms x{s[0]}" for n, s in stats.items() if s[0]))
     return ms, stats
+
+
+def time_step_prepare(ctx, wl, reps=30):
+    """Host time of the library's step-metadata producer (Transformer.preparePrefill /
+    prepareDecode restated in C++, plus the one upload) for the workload's scheduler state.  The
+    nva_seq array is built once, as a Java caller would keep its tables in native memory; the
+    timed region is the C call alone."""
+    import torch
+    from types import SimpleNamespace
+    from nanollvm_amd import _native as N
+    from nanollvm_amd.step import seq_array
+    seqs = [SimpleNamespace(seq_id=b, num_tokens=c + n, num_cached_tokens=c,
+                            num_scheduled_tokens=n, block_table=wl.tables[b])
+            for b, (c, n) in enumerate(wl.seqs)]
+    arr, keep = seq_array(seqs)
+    lib = N.load()
+    fn = lib.nva_step_prepare_prefill if wl.meta.is_prefill else lib.nva_step_prepare_decode
+    assert fn(ctx.handle, arr, len(seqs), wl.block_size) == N.NVA_OK
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn(ctx.handle, arr, len(seqs), wl.block_size)
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    del keep
+    m = wl.meta
+    tokens = len(m.positions)
+    pages = int(sum(len(t) for t in wl.tables))
+    bt = m.block_tables.size if m.block_tables is not None else 0
+    upload = 4 * (tokens * 2 + bt + 2 * (len(wl.seqs) + 1) + len(wl.seqs))
+    return {"build_upload_us": round((t1 - t0) / reps * 1e6, 1), "sequences": len(wl.seqs),
+            "tokens": tokens, "pages": pages, "upload_bytes": upload}
+
+
+def kernel_a_roofline(wl, stats):
+    n, t = stats["rope_store"]
+    ms = t / max(n, 1)
+    byts = kernel_a_bytes(wl, False)
+    gbs = byts / (ms * 1e-3) / 1e9
+    return {"kernel": "rope_store_kernel (q/k RMSNorm + RoPE + K/V store)", "bound": "hbm",
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": byts,
+            "ms": round(ms, 5)}
 
 
 def bench_decode(args, ctx):
@@ -176,6 +246,8 @@ def bench_decode(args, ctx):
                      "traffic": measured_traffic("decode"),
                      "kernel": "row_attention_kernel<128,2> (split-KV decode)",
                      "algorithmic_bytes_per_launch": byts},
+        "kernel_a": kernel_a_roofline(wl, stats),
+        "step_metadata": time_step_prepare(ctx, wl),
     }
     rope.close()
     arena.close()
@@ -217,6 +289,8 @@ def bench_prefill(args, ctx):
                      "traffic": measured_traffic("prefill"),
                      "kernel": "prefill_kernel<128,2> (fp32 MFMA 16x16x4, 8 waves)",
                      "algorithmic_flops_per_launch": flops},
+        "kernel_a": kernel_a_roofline(wl, stats),
+        "step_metadata": time_step_prepare(ctx, wl),
     }
     rope.close()
     arena.close()
@@ -322,6 +396,8 @@ def main():
             "tokens_per_s_per_layer": round(len(wl.seqs) / (dec["ms"] * 1e-3), 1),
             "kernel_ms": {n: round(x, 5) for n, x in dec["kernel_ms"].items()},
             "roofline": dec["roofline"],
+            "kernel_a": dec["kernel_a"],
+            "step_metadata": dec["step_metadata"],
         })
     else:
         line.update({"value": pf["tflops"], "unit": "TFLOP/s", "ms_per_step": pf["ms_per_step"],

@@ -143,6 +143,65 @@ nva_status nva_step_set(nva_ctx *ctx, int is_prefill, const int32_t *cu_q, const
                         const int32_t *context_lens, const int32_t *block_tables,
                         int bt_stride, const int32_t *seq_ids, const float *positions,
                         int num_tokens);
+/* One scheduled sequence as the model runner sees it (engine/Sequence.java): host arrays.
+ *   num_tokens         Sequence.numTokens(): every token of the sequence so far
+ *   num_cached_tokens  prefill: tokens already in the pages (numCachedTokens)
+ *   num_scheduled      prefill: tokens of this step's chunk (numScheduledTokens)
+ *   block_table        the sequence's block ids (blockTable()), num_blocks entries */
+typedef struct nva_seq {
+  int32_t seq_id;
+  int32_t num_tokens;
+  int32_t num_cached_tokens;
+  int32_t num_scheduled;
+  const int32_t *block_table;
+  int32_t num_blocks;
+} nva_seq;
+
+/* Step metadata as Context.set receives it, in caller-owned host arrays:
+ *   cu_q, cu_k        [num_seqs + 1]   (prefill)
+ *   slot_mapping      [tokens]         num_slots entries are written
+ *   context_lens      [num_seqs]       (decode)
+ *   seq_ids           [tokens]
+ *   positions         [tokens]         fp32, as the step's positions tensor
+ *   block_tables      [num_seqs * max(num_blocks)], -1 padded; bt_stride = max(num_blocks);
+ *                     has_tables = 0 when the reference attaches none (prefill with no cached
+ *                     prefix) */
+typedef struct nva_step_meta {
+  int32_t *cu_q, *cu_k;
+  int32_t max_seqlen_q, max_seqlen_k;
+  int32_t *slot_mapping;
+  int32_t num_slots;
+  int32_t *context_lens;
+  int32_t *seq_ids;
+  float *positions;
+  int32_t num_tokens;
+  int32_t *block_tables;
+  int32_t bt_stride;
+  int32_t has_tables;
+} nva_step_meta;
+
+/* Transformer.preparePrefill, engine/Transformer.java:342-418 (with prepareBlockTables,
+ * :319-330): for each sequence the window [numCachedTokens, numCachedTokens + numScheduled)
+ * gives positions, seq ids, cu_seqlens (Q: new tokens, K: full context through the window end)
+ * and the slot of every new token in the sequence's pages (a sequence with an empty block table
+ * adds no slots); block tables are attached only when cu_k.last > cu_q.last and some sequence
+ * has a table.  Pure host code (no device, no context).  NVA_E_ARG where Java would throw
+ * (a block table too short for the window). */
+nva_status nva_build_prefill_metadata(const nva_seq *seqs, int num_seqs, int block_size,
+                                      nva_step_meta *out);
+/* Transformer.prepareDecode, engine/Transformer.java:427-456: one row per sequence with
+ * position numTokens - 1, context length numTokens, and the slot
+ * blockTable.last * blockSize + lastBlockNumTokens - 1 (Sequence.java:323-335); block tables
+ * always attached.  NVA_E_ARG for an empty block table (Java: NoSuchElementException). */
+nva_status nva_build_decode_metadata(const nva_seq *seqs, int num_seqs, int block_size,
+                                     nva_step_meta *out);
+/* The two producers above followed by nva_step_set: the per-step metadata of a scheduler step
+ * built on the host and uploaded in one transfer. */
+nva_status nva_step_prepare_prefill(nva_ctx *ctx, const nva_seq *seqs, int num_seqs,
+                                    int block_size);
+nva_status nva_step_prepare_decode(nva_ctx *ctx, const nva_seq *seqs, int num_seqs,
+                                   int block_size);
+
 /* Replaces the step's positions only (the positions tensor RotaryEmbedding.forward receives,
  * Norms.java:275, rounded with Math.round as at Norms.java:317).  Valid after nva_step_set. */
 nva_status nva_step_positions(nva_ctx *ctx, const float *positions, int num_tokens);

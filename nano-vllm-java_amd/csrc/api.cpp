@@ -763,6 +763,12 @@ int32_t java_round(float x) {
 
 }  // namespace
 
+// Records msg as the context's last error (the step producers in step.cpp report through it).
+__attribute__((visibility("hidden"))) nva_status nva_internal_fail(nva_ctx *ctx, nva_status st,
+                                                                 const char *msg) {
+  return fail(ctx, st, "%s", msg);
+}
+
 extern "C" {
 
 const char *nva_status_string(nva_status s) {

@@ -60,6 +60,43 @@ class RmsNormDesc(ctypes.Structure):
 
 _pnorm = ctypes.POINTER(RmsNormDesc)
 
+
+class Seq(ctypes.Structure):
+    """nva_seq: one scheduled sequence (engine/Sequence.java) with its block table."""
+
+    _fields_ = [
+        ("seq_id", ctypes.c_int32),
+        ("num_tokens", ctypes.c_int32),
+        ("num_cached_tokens", ctypes.c_int32),
+        ("num_scheduled", ctypes.c_int32),
+        ("block_table", ctypes.c_void_p),
+        ("num_blocks", ctypes.c_int32),
+    ]
+
+
+class StepMetaOut(ctypes.Structure):
+    """nva_step_meta: caller-owned host arrays the step producers fill."""
+
+    _fields_ = [
+        ("cu_q", ctypes.c_void_p),
+        ("cu_k", ctypes.c_void_p),
+        ("max_seqlen_q", ctypes.c_int32),
+        ("max_seqlen_k", ctypes.c_int32),
+        ("slot_mapping", ctypes.c_void_p),
+        ("num_slots", ctypes.c_int32),
+        ("context_lens", ctypes.c_void_p),
+        ("seq_ids", ctypes.c_void_p),
+        ("positions", ctypes.c_void_p),
+        ("num_tokens", ctypes.c_int32),
+        ("block_tables", ctypes.c_void_p),
+        ("bt_stride", ctypes.c_int32),
+        ("has_tables", ctypes.c_int32),
+    ]
+
+
+_pseq = ctypes.POINTER(Seq)
+_pmeta = ctypes.POINTER(StepMetaOut)
+
 SIGNATURES = {
     "nva_ctx_create": ([_ci, _pvp], _st),
     "nva_ctx_destroy": ([_vp], _st),
@@ -89,6 +126,10 @@ SIGNATURES = {
     "nva_rope_attention_forward": ([_vp, _vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci,
                                     _vp, _vp, _vp], _st),
     "nva_rms_norm_forward": ([_vp, _pnorm, _vp, _ci, _ci, _vp], _st),
+    "nva_build_prefill_metadata": ([_pseq, _ci, _ci, _pmeta], _st),
+    "nva_build_decode_metadata": ([_pseq, _ci, _ci, _pmeta], _st),
+    "nva_step_prepare_prefill": ([_vp, _pseq, _ci, _ci], _st),
+    "nva_step_prepare_decode": ([_vp, _pseq, _ci, _ci], _st),
     "nva_norm_rope_attention_forward": ([_vp, _vp, _vp, _pnorm, _pnorm, _pnorm,
                                          ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci, _vp, _vp,
                                          _vp], _st),

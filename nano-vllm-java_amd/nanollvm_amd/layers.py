@@ -158,6 +158,25 @@ class Context:
             _ptr(bt), stride, _ptr(ids), _ptr(pos), ntok), "Context.set")
         self._positions_key = None if pos is None else pos.tobytes()
 
+    def prepare_prefill(self, seqs, block_size: int) -> None:
+        """Transformer.preparePrefill + Context.set (Transformer.java:342-418) in the library:
+        ``seqs`` are engine.Sequence objects with numCachedTokens / numScheduledTokens set."""
+        from .step import seq_array
+        arr, keep = seq_array(seqs)
+        _check(self._h, N.load().nva_step_prepare_prefill(self._h, arr, len(seqs), block_size),
+               "Transformer.preparePrefill")
+        del keep
+        self._positions_key = None
+
+    def prepare_decode(self, seqs, block_size: int) -> None:
+        """Transformer.prepareDecode + Context.set (Transformer.java:427-456) in the library."""
+        from .step import seq_array
+        arr, keep = seq_array(seqs)
+        _check(self._h, N.load().nva_step_prepare_decode(self._h, arr, len(seqs), block_size),
+               "Transformer.prepareDecode")
+        del keep
+        self._positions_key = None
+
     def set_positions(self, positions) -> None:
         pos = np.ascontiguousarray(
             positions.detach().cpu().numpy() if isinstance(positions, torch.Tensor) else positions,
