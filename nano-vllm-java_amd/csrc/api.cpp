@@ -1178,7 +1178,7 @@ nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, 
   a.hk = hk;
   a.head_dim = rope->head_size;
   Timed tm(ctx, "rope_store");
-  HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "rope kernel launch");
+  HIP_TRY(ctx, launch_rope_store(a, ctx->stream, ctx->num_cus), "rope kernel launch");
   tm.done();
   return NVA_OK;
 }
@@ -1213,7 +1213,7 @@ nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *
     a.hk = d.num_kv_heads;
     a.head_dim = d.head_dim;
     Timed tm(ctx, "store");
-    HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "store kernel launch");
+    HIP_TRY(ctx, launch_rope_store(a, ctx->stream, ctx->num_cus), "store kernel launch");
     tm.done();
   }
   return attention_after_store(ctx, kv, d, q, k, v, num_tokens, out);
@@ -1245,6 +1245,9 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
       (q_out && !aligned16(q_out)) || (k_out && !aligned16(k_out)))
     return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
+  for (const nva_rms_norm *n : {q_norm, k_norm, v_norm})
+    if (n && n->weight && !aligned16(n->weight))
+      return fail(ctx, NVA_E_ARG, "RMSNorm weights must be 16-byte aligned device pointers");
   st = check_positions(ctx, num_tokens, rope->max_pos);
   if (st != NVA_OK) return st;
   const nva_attn_desc d = *desc;
@@ -1296,7 +1299,7 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
                 "kernel's %zu-byte LDS budget", a.hq, a.hk, a.head_dim, kRopeNormMaxLds);
   {
     Timed tm(ctx, "rope_store");
-    HIP_TRY(ctx, launch_rope_store(a, ctx->stream), "rope_store kernel launch");
+    HIP_TRY(ctx, launch_rope_store(a, ctx->stream, ctx->num_cus), "rope_store kernel launch");
     tm.done();
   }
   return attention_after_store(ctx, kv, d, q_out, k_out, v_out ? v_out : v, num_tokens, out);

@@ -112,6 +112,7 @@ struct RopeStoreLaunch {
   const float *cos_sin;       // [max_pos, d]
   int32_t tokens, hq, hk, head_dim;
   HeadNorm qn, kn, vn;        // per-head RMSNorm applied to q, k, v before rotation / store
+  int32_t iters_per_wg;       // row kernel: row iterations per workgroup (set by the launcher)
 };
 
 // Standalone RMSNorm over rows of any width (RMSNorm.forward).
@@ -130,7 +131,7 @@ struct GatherLaunch {
 };
 
 // Kernel launchers (each returns the hipGetLastError() of its launch).
-hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s);
+hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s, int num_cus);
 hipError_t launch_rms_norm(const NormLaunch &a, hipStream_t s);
 // LDS bytes the fused kernel needs for its head norms (0 when no norm is enabled).
 size_t rope_store_norm_lds(const RopeStoreLaunch &a);

@@ -44,9 +44,16 @@ __device__ __forceinline__ float norm1(float x, float inv, const HeadNorm &n, in
   return y;
 }
 
+// Four consecutive elements starting at j (j % 4 == 0; the weight is 16-byte aligned).
 __device__ __forceinline__ float4 norm4(float4 x, float inv, const HeadNorm &n, int j) {
-  return make_float4(norm1(x.x, inv, n, j), norm1(x.y, inv, n, j + 1), norm1(x.z, inv, n, j + 2),
-                     norm1(x.w, inv, n, j + 3));
+  float4 y = make_float4(mul_rn(x.x, inv), mul_rn(x.y, inv), mul_rn(x.z, inv), mul_rn(x.w, inv));
+  if (n.weight) {
+    float4 w = ld4(n.weight + j);
+    if (n.one_plus)
+      w = make_float4(add_rn(1.0f, w.x), add_rn(1.0f, w.y), add_rn(1.0f, w.z), add_rn(1.0f, w.w));
+    y = make_float4(mul_rn(y.x, w.x), mul_rn(y.y, w.y), mul_rn(y.z, w.z), mul_rn(y.w, w.w));
+  }
+  return y;
 }
 
 // ((x0*x0 + x1*x1) + x2*x2) + x3*x3, the group sum of ScalarFloatKernels.sumSquares.
@@ -65,6 +72,17 @@ __device__ __forceinline__ float rms_inv(const float *groups, int ngroups, const
   for (int i = 4 * ngroups; i < d; i++) sum = add_rn(sum, mul_rn(x[i], x[i]));
   const float var = sum / (float)d;  // correctly rounded (HIP default)
   return (float)(1.0 / sqrt((double)add_rn(var, eps)));
+}
+
+// The value of lane ^ X (X = half a row group): DPP within a quad or row, a bit-mode swizzle
+// across the two 16-lane rows of a 32-lane half, a lane permute for the two halves of a wave.
+template <int X>
+__device__ __forceinline__ float partner(float v) {
+  if constexpr (X == 1) return __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false);
+  if constexpr (X == 2) return __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false);
+  if constexpr (X == 16)
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  return __shfl_xor(v, X);
 }
 
 }  // namespace
@@ -215,6 +233,152 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
   }
 }
 
+// The same work with one group of LPR lanes per head row (q, k or v row of one token) and no
+// LDS or barriers.  Workgroup (t, s) handles token t's rows: row group g takes rows
+// g + RPB * i for the iterations i of slice s (the host sizes the slices so that small batches
+// still fill the chip), loading four rows at a time.  The token's cos|sin row, position and
+// slot are loaded once per lane and reused by every row.  Lane c of a group holds the float4
+// groups c + LPR * j (j < VPL) of the row.  The norm's group sums are folded in index order with
+// DPP shifts; the rotation partner of a first-half element sits LPR / 2 lanes away (VPL = 1) or
+// in the lane's own second float4 (VPL = 2, d = 512).
+template <int LPR, int VPL>
+__global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
+  constexpr int D = 4 * LPR * VPL;
+  constexpr int HALF = D / 2;
+  constexpr int RPB = 256 / LPR;  // row groups per workgroup
+  constexpr int NR = 4;           // rows loaded together
+  const int t = blockIdx.x;
+  const int c = threadIdx.x % LPR;
+  const int grp = threadIdx.x / LPR;
+  const int base = (threadIdx.x & 63) - c;  // first lane of this row group in the wave
+  const int rq = a.q ? a.hq : 0;
+  const int rk = a.k ? a.hk : 0;
+  const bool store_any = a.k_cache != nullptr;
+  const int rv = (a.v && (store_any || a.v_out)) ? a.hk : 0;
+  const int rows = rq + rk + rv;
+  const int iters = (rows + RPB - 1) / RPB;
+  const int it0 = blockIdx.y * a.iters_per_wg;
+  const int it1 = min(iters, it0 + a.iters_per_wg);
+  const size_t krow = (size_t)a.hk * D;
+
+  const bool rotate = a.positions != nullptr;
+  float4 cv[VPL], sv[VPL];
+  if (rotate) {
+    const float *cs = a.cos_sin + (size_t)a.positions[t] * D;
+    // VPL == 1: lane c < LPR/2 rotates x1 = elements 4c.., the others x2 = HALF + 4(c - LPR/2).
+    const int i0 = VPL == 1 ? 4 * (c < LPR / 2 ? c : c - LPR / 2) : 4 * c;
+    cv[0] = ld4(cs + i0);
+    sv[0] = ld4(cs + HALF + i0);
+  }
+  const int32_t slot = a.slots ? a.slots[t] : -1;
+  const bool store = store_any && slot >= 0;
+
+  for (int ib = it0; ib < it1; ib += NR) {
+    int kind[NR], h[NR];
+    bool live[NR];
+    float4 x[NR][VPL];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      const int r = grp + RPB * (ib + i);
+      live[i] = ib + i < it1 && r < rows;  // uniform over the row group
+      const int rc = live[i] ? r : 0;
+      kind[i] = rc < rq ? 0 : (rc < rq + rk ? 1 : 2);  // q, k, v
+      h[i] = kind[i] == 0 ? rc : (kind[i] == 1 ? rc - rq : rc - rq - rk);
+      const int heads = kind[i] == 0 ? a.hq : a.hk;
+      const float *src = (kind[i] == 0 ? a.q : (kind[i] == 1 ? a.k : a.v)) +
+                         ((size_t)t * heads + h[i]) * D;
+#pragma unroll
+      for (int j = 0; j < VPL; j++)
+        x[i][j] = live[i] ? ld4(src + 4 * (c + LPR * j)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      if (ib + i >= it1) break;  // uniform over the workgroup (the DPP fold spans the wave)
+      const HeadNorm &nm = kind[i] == 0 ? a.qn : (kind[i] == 1 ? a.kn : a.vn);
+      if (nm.enabled) {
+        // ScalarFloatKernels.sumSquares order: group sums added in group-index order.
+        float sum = 0.0f;
+        if constexpr (VPL == 1) {
+          // Serial fold as a shift-and-add chain: after step s, lane j holds the in-order sum
+          // of the s group sums ending at lane j, starting from 0 (lane 0 shifts in 0), so
+          // after LPR steps the group's last lane holds ((0 + p0) + p1) + ... + p[LPR-1] --
+          // the same additions in the same order, with no LDS traffic.
+          const float p = group_sq(x[i][0].x, x[i][0].y, x[i][0].z, x[i][0].w);
+          float acc = 0.0f;
+#pragma unroll
+          for (int l = 0; l < LPR; l++)
+            acc = add_rn(__builtin_amdgcn_update_dpp(0.0f, acc, 0x138, 0xF, 0xF, false), p);
+          sum = __shfl(acc, base + LPR - 1);
+        } else {
+#pragma unroll
+          for (int j = 0; j < VPL; j++) {
+            const float p = group_sq(x[i][j].x, x[i][j].y, x[i][j].z, x[i][j].w);
+#pragma unroll
+            for (int l = 0; l < LPR; l++) sum = add_rn(sum, __shfl(p, base + l));
+          }
+        }
+        const float var = sum / (float)D;  // correctly rounded (HIP default)
+        const float inv = (float)(1.0 / sqrt((double)add_rn(var, nm.eps)));
+#pragma unroll
+        for (int j = 0; j < VPL; j++) x[i][j] = norm4(x[i][j], inv, nm, 4 * (c + LPR * j));
+      }
+
+      float4 o[VPL];
+      if (kind[i] != 2 && rotate) {
+        if constexpr (VPL == 1) {
+          // Partner = the other half of the row.
+          float4 y;
+          y.x = partner<LPR / 2>(x[i][0].x);
+          y.y = partner<LPR / 2>(x[i][0].y);
+          y.z = partner<LPR / 2>(x[i][0].z);
+          y.w = partner<LPR / 2>(x[i][0].w);
+          if (c < LPR / 2) {  // o[i] = x1*cos - x2*sin
+            o[0].x = x[i][0].x * cv[0].x - y.x * sv[0].x;
+            o[0].y = x[i][0].y * cv[0].y - y.y * sv[0].y;
+            o[0].z = x[i][0].z * cv[0].z - y.z * sv[0].z;
+            o[0].w = x[i][0].w * cv[0].w - y.w * sv[0].w;
+          } else {            // o[h+i] = x2*cos + x1*sin
+            o[0].x = x[i][0].x * cv[0].x + y.x * sv[0].x;
+            o[0].y = x[i][0].y * cv[0].y + y.y * sv[0].y;
+            o[0].z = x[i][0].z * cv[0].z + y.z * sv[0].z;
+            o[0].w = x[i][0].w * cv[0].w + y.w * sv[0].w;
+          }
+        } else {
+          // VPL == 2: x[0] = elements [4c, 4c+4) (first half), x[1] = [HALF + 4c, +4).
+          o[0].x = x[i][0].x * cv[0].x - x[i][1].x * sv[0].x;
+          o[0].y = x[i][0].y * cv[0].y - x[i][1].y * sv[0].y;
+          o[0].z = x[i][0].z * cv[0].z - x[i][1].z * sv[0].z;
+          o[0].w = x[i][0].w * cv[0].w - x[i][1].w * sv[0].w;
+          o[1].x = x[i][1].x * cv[0].x + x[i][0].x * sv[0].x;
+          o[1].y = x[i][1].y * cv[0].y + x[i][0].y * sv[0].y;
+          o[1].z = x[i][1].z * cv[0].z + x[i][0].z * sv[0].z;
+          o[1].w = x[i][1].w * cv[0].w + x[i][0].w * sv[0].w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) o[j] = x[i][j];
+      }
+      if (!live[i]) continue;
+      const int heads = kind[i] == 0 ? a.hq : a.hk;
+      const size_t row = ((size_t)t * heads + h[i]) * D;
+#pragma unroll
+      for (int j = 0; j < VPL; j++) {
+        const int e = 4 * (c + LPR * j);
+        if (kind[i] == 0) {
+          st4(a.q_out + row + e, o[j]);
+        } else if (kind[i] == 1) {
+          if (a.k_out) st4(a.k_out + row + e, o[j]);
+          if (store) st4(a.k_cache + (size_t)slot * krow + (size_t)h[i] * D + e, o[j]);
+        } else {
+          if (store) st4(a.v_cache + (size_t)slot * krow + (size_t)h[i] * D + e, o[j]);
+          if (a.v_out) st4(a.v_out + row + e, o[j]);
+        }
+      }
+    }
+  }
+}
+
 // RMSNorm.forward over rows of any width (Ops.java:444-500): one workgroup per row; the group
 // sums of each 1024-group chunk go through LDS and one lane adds them in the reference's order.
 __global__ void __launch_bounds__(256) rms_norm_kernel(NormLaunch a) {
@@ -264,8 +428,43 @@ size_t rope_store_norm_lds(const RopeStoreLaunch &a) {
   return rows * ((size_t)(a.head_dim >> 2) + 1) * sizeof(float);
 }
 
-hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s) {
+namespace {
+
+template <int LPR, int VPL>
+hipError_t launch_rows(const RopeStoreLaunch &a, hipStream_t s, int num_cus) {
+  const int rq = a.q ? a.hq : 0;
+  const int rk = a.k ? a.hk : 0;
+  const int rv = (a.v && (a.k_cache || a.v_out)) ? a.hk : 0;
+  const int rows = rq + rk + rv;
+  if (rows <= 0) return hipSuccess;
+  constexpr int RPB = 256 / LPR;
+  const int iters = (rows + RPB - 1) / RPB;
+  // Split a token's rows over several workgroups only when the batch alone would leave the
+  // chip short of about four workgroups per CU.
+  int slices = 1;
+  while (slices < iters && (int64_t)a.tokens * slices < 4LL * num_cus) slices++;
+  RopeStoreLaunch b = a;
+  b.iters_per_wg = (iters + slices - 1) / slices;
+  const int grid_y = (iters + b.iters_per_wg - 1) / b.iters_per_wg;
+  hipLaunchKernelGGL((rope_rows_kernel<LPR, VPL>), dim3(a.tokens, grid_y), dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s, int num_cus) {
   if (a.tokens <= 0) return hipSuccess;
+  // Row kernel for the head dims it is instantiated for; the per-token kernel otherwise.
+  switch (a.head_dim) {
+    case 8: return launch_rows<2, 1>(a, s, num_cus);
+    case 16: return launch_rows<4, 1>(a, s, num_cus);
+    case 32: return launch_rows<8, 1>(a, s, num_cus);
+    case 64: return launch_rows<16, 1>(a, s, num_cus);
+    case 128: return launch_rows<32, 1>(a, s, num_cus);
+    case 256: return launch_rows<64, 1>(a, s, num_cus);
+    case 512: return launch_rows<64, 2>(a, s, num_cus);
+    default: break;
+  }
   const size_t lds = rope_store_norm_lds(a);
   if (lds > kRopeNormMaxLds) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rope_store_kernel, dim3(a.tokens), dim3(128), lds, s, a);
