@@ -241,6 +241,15 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
 nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const float *x, int rows,
                                 int width, float *out);
 
+/* Linear.Row.forward (o_proj), models/internal/Qwen3ForCausalLM.java:221 -> Ops.linear,
+ * tensor/Ops.java:84-124 -> MatmulRuntime.linear, tensor/MatmulRuntime.java:234-255:
+ * y[rows, out] = x[rows, in] weight[out, in]^T (+ bias[out]).  x, weight, bias and y are
+ * DEVICE pointers (x and weight 16-byte aligned, in % 4 == 0); bias may be NULL.  x is
+ * typically the attention output [tokens, num_heads * head_dim] used in place.  fp32 on MFMA;
+ * the sum order differs from the reference's gemv panels (fp32 rounding only). */
+nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
+                              const float *weight, int out, const float *bias, float *y);
+
 /* The per-head q/k (and Gemma 4 v) RMSNorm, RotaryEmbedding.forward and Attention.forward as
  * one call, the way the model layers chain them (Qwen3Attention.forward,
  * models/internal/Qwen3ForCausalLM.java:207-227 normHeads; Gemma3ForCausalLM.java:143-157;

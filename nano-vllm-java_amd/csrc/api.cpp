@@ -166,6 +166,7 @@ struct nva_ctx {
   DevBuf d_q_rot;    // fused path scratch for rotated q
   DevBuf d_k_rot;    // fused path scratch for rotated k
   DevBuf d_v_norm;   // fused path scratch for normalised v (dense prefill with a v norm)
+  DevBuf d_lin;      // split-K partial sums of the linear kernel
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
 
   bool timing = false;
@@ -825,6 +826,7 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   ctx->d_q_rot.release();
   ctx->d_k_rot.release();
   ctx->d_v_norm.release();
+  ctx->d_lin.release();
   ctx->d_gather.release();
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
@@ -1303,6 +1305,49 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
     tm.done();
   }
   return attention_after_store(ctx, kv, d, q_out, k_out, v_out ? v_out : v, num_tokens, out);
+}
+
+nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
+                              const float *weight, int out, const float *bias, float *y) {
+  if (!ctx) return NVA_E_ARG;
+  if (rows < 0 || in <= 0 || out <= 0)
+    return fail(ctx, NVA_E_ARG, "bad linear shape rows=%d in=%d out=%d", rows, in, out);
+  if (rows == 0) return NVA_OK;
+  if (!x || !weight || !y) return fail(ctx, NVA_E_ARG, "x, weight and y are required");
+  if (in % 4 != 0)
+    return fail(ctx, NVA_E_UNSUPPORTED, "linear needs in %% 4 == 0 (got %d)", in);
+  if (!aligned16(x) || !aligned16(weight))
+    return fail(ctx, NVA_E_ARG, "x and weight must be 16-byte aligned device pointers");
+  // Split K only when the tile grid alone leaves the chip short of two workgroups per CU (the
+  // resident limit at 64 KB of LDS each); every slice keeps at least 4 K tiles.
+  const int64_t tiles = (int64_t)((out + linear_tile_cols() - 1) / linear_tile_cols()) *
+                        ((rows + linear_tile_rows() - 1) / linear_tile_rows());
+  const int bk = linear_k_tile();
+  const int nkt = (in + bk - 1) / bk;
+  const int64_t want = 2LL * ctx->num_cus;
+  int splits = (int)std::min<int64_t>(std::max<int64_t>(1, (want + tiles - 1) / tiles),
+                                      std::max(1, nkt / 4));
+  const int kt_per = (nkt + splits - 1) / splits;
+  splits = (nkt + kt_per - 1) / kt_per;
+  LinearLaunch a{};
+  a.x = x;
+  a.w = weight;
+  a.bias = bias;
+  a.y = y;
+  a.m = rows;
+  a.n = out;
+  a.k = in;
+  a.splits = splits;
+  a.k_per_split = kt_per * bk;
+  if (splits > 1) {
+    HIP_TRY(ctx, ctx->d_lin.reserve((size_t)splits * rows * out * sizeof(float)),
+            "linear partial buffer");
+    a.part = static_cast<float *>(ctx->d_lin.ptr);
+  }
+  Timed tm(ctx, "linear");
+  HIP_TRY(ctx, launch_linear(a, ctx->stream), "linear kernel launch");
+  tm.done();
+  return NVA_OK;
 }
 
 nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const float *x, int rows,

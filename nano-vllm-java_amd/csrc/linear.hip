@@ -1,0 +1,198 @@
+// Linear.Row (o_proj): y[M, N] = x[M, K] W[N, K]^T (+ bias) in fp32 on MFMA.
+//
+// Semantics (tensor/Ops.java:84-124 linear, tensor/MatmulRuntime.java:234-255): W is the
+// row-major [out, in] weight, x the [rows, in] activations (the attention output
+// [T, Hq * d], used in place), y a fresh [rows, out]; y = x W^T + bias.  The reference sums each
+// output in its gemv panel order; here the sum runs over MFMA steps and split-K slices, so the
+// result agrees to fp32 rounding (checked against the oracle within the attention tolerance).
+//
+// Mapping onto CDNA4.  A workgroup (4 waves, 256 threads) owns a 128 x 128 tile of y and one
+// K slice; wave (wm, wn) computes 64 x 64 of it as 2 x 2 blocks of v_mfma_f32_32x32x2_f32.
+//   * x and W are both K-contiguous, so the A operand (x rows) and the B operand (W rows) are
+//     read the same way: for each 8-wide K chunk a lane (i, h) reads one float4 of its row
+//     (elements 4h .. 4h + 3), which feeds 4 MFMA steps -- step s contracts k = 4h + s, a
+//     permutation of the chunk that A and B share.
+//   * K tiles of 32 are copied HBM -> LDS with global_load_lds_dwordx4, double-buffered, one
+//     barrier per tile; each 128-byte row of a tile has its 16-byte chunks XOR-swizzled by
+//     (row & 7), so the 8 lanes of a ds_read_b128 phase hit 8 different bank groups.
+//   * Output block layout (32 x 32, 16 values per lane): value r of lane (i, h) is row
+//     8 * (r / 4) + 4 * h + r % 4, column i -- lanes 0..31 write 128 contiguous bytes.
+//   * When the tile grid alone cannot fill the chip (decode: a few rows), K is split over
+//     blockIdx.z; slices write partial sums and linear_reduce_kernel adds them in slice order,
+//     plus the bias.  (Letting the last slice of a tile reduce in place needs a device-scope
+//     release per slice, which on this multi-XCD part writes back L2 and cost more than the
+//     separate launch.)
+// Algorithmic work: 2 * M * N * K flops; HBM bytes (once): 4 * (M * K + N * K + M * N).
+#include "nva_internal.h"
+
+namespace nva {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32;
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+}  // namespace
+
+__global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
+  __shared__ __attribute__((aligned(16))) float sa0[BM * BK];
+  __shared__ __attribute__((aligned(16))) float sb0[BN * BK];
+  __shared__ __attribute__((aligned(16))) float sa1[BM * BK];
+  __shared__ __attribute__((aligned(16))) float sb1[BN * BK];
+
+  const int n0 = blockIdx.x * BN;
+  const int m0 = blockIdx.y * BM;
+  const int kb = blockIdx.z * a.k_per_split;
+  const int ke = min(a.k, kb + a.k_per_split);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int i = lane & 31;  // MFMA row (A) / column (B) index of this lane
+  const int h = lane >> 5;  // which half of an 8-wide K chunk this lane supplies
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+    for (int bn = 0; bn < 2; bn++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[bm][bn][r] = 0.0f;
+
+  // Copy instruction p of wave w moves rows [8g, 8g + 8) of a tile, g = 4p + w: lane l takes
+  // row 8g + l / 8, LDS chunk position l % 8, i.e. global chunk (l % 8) ^ (row & 7).
+  const int lrow = lane >> 3;
+  const int lpos = lane & 7;
+  auto issue = [&](int kt, float *da, float *db) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int g = 4 * p + wave;
+      const int r = 8 * g + lrow;
+      int kc = kt + 4 * (lpos ^ (r & 7));
+      kc = kc < ke ? kc : kb;  // past the slice: a valid address, zeroed at use
+      const int xr = min(m0 + r, a.m - 1);
+      const int wr = min(n0 + r, a.n - 1);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)(a.x + (size_t)xr * a.k + kc),
+          (__attribute__((address_space(3))) void *)(da + g * 8 * BK), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)(a.w + (size_t)wr * a.k + kc),
+          (__attribute__((address_space(3))) void *)(db + g * 8 * BK), 16, 0, 0);
+    }
+  };
+
+  auto compute = [&](int kt, const float *sa, const float *sb) {
+#pragma unroll
+    for (int kk = 0; kk < BK / 8; kk++) {
+      const int c = 2 * kk + h;  // this lane's 16-byte chunk of the row
+      const bool valid = kt + 4 * c < ke;
+      float4 av[2], bv[2];
+#pragma unroll
+      for (int b = 0; b < 2; b++) {
+        const int ra = wm * 64 + b * 32 + i;
+        const int rb = wn * 64 + b * 32 + i;
+        av[b] = ld4(sa + ra * BK + 4 * (c ^ (ra & 7)));
+        bv[b] = ld4(sb + rb * BK + 4 * (c ^ (rb & 7)));
+        if (!valid) {
+          av[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+          bv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+        for (int bn = 0; bn < 2; bn++) {
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].x, bv[bn].x, acc[bm][bn], 0, 0, 0);
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].y, bv[bn].y, acc[bm][bn], 0, 0, 0);
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].z, bv[bn].z, acc[bm][bn], 0, 0, 0);
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].w, bv[bn].w, acc[bm][bn], 0, 0, 0);
+        }
+    }
+  };
+
+  const int ntiles = (ke - kb + BK - 1) / BK;
+  if (ntiles > 0) issue(kb, sa0, sb0);
+  for (int t = 0; t < ntiles; t += 2) {
+    const int kt = kb + t * BK;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 1 < ntiles) issue(kt + BK, sa1, sb1);
+    compute(kt, sa0, sb0);
+    if (t + 1 >= ntiles) break;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 2 < ntiles) issue(kt + 2 * BK, sa0, sb0);
+    compute(kt + BK, sa1, sb1);
+  }
+
+  const bool direct = a.splits == 1;
+  float *dst = direct ? a.y : a.part + (size_t)blockIdx.z * a.m * a.n;
+#pragma unroll
+  for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+    for (int bn = 0; bn < 2; bn++) {
+      const int col = n0 + wn * 64 + bn * 32 + i;
+      if (col >= a.n) continue;
+      const float bias = direct && a.bias ? a.bias[col] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row < a.m) dst[(size_t)row * a.n + col] = acc[bm][bn][r] + bias;
+      }
+    }
+}
+
+// y = bias + sum over slices of the partials, slices added in order; four outputs per thread
+// when a row is a multiple of 4 floats, so every load is a float4 and the slices' loads are
+// independent.
+__global__ void __launch_bounds__(256) linear_reduce_kernel(LinearLaunch a) {
+  const size_t plane = (size_t)a.m * a.n;
+  const bool vec = (a.n & 3) == 0;
+  const size_t units = vec ? plane / 4 : plane;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += stride) {
+    if (vec) {
+      const size_t idx = 4 * u;
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int z = 0; z < a.splits; z++) {
+        const float4 p = *reinterpret_cast<const float4 *>(a.part + (size_t)z * plane + idx);
+        s.x += p.x;
+        s.y += p.y;
+        s.z += p.z;
+        s.w += p.w;
+      }
+      if (a.bias) {
+        const int col = (int)(idx % a.n);
+        s.x += a.bias[col];
+        s.y += a.bias[col + 1];
+        s.z += a.bias[col + 2];
+        s.w += a.bias[col + 3];
+      }
+      *reinterpret_cast<float4 *>(a.y + idx) = s;
+    } else {
+      float s = 0.0f;
+      for (int z = 0; z < a.splits; z++) s += a.part[(size_t)z * plane + u];
+      a.y[u] = a.bias ? s + a.bias[u % a.n] : s;
+    }
+  }
+}
+
+hipError_t launch_linear(const LinearLaunch &a, hipStream_t s) {
+  if (a.m <= 0 || a.n <= 0) return hipSuccess;
+  const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM, a.splits);
+  hipLaunchKernelGGL(linear_kernel, grid, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  const size_t units = (a.n & 3) == 0 ? (size_t)a.m * a.n / 4 : (size_t)a.m * a.n;
+  const unsigned blocks = (unsigned)std::min<size_t>((units + 255) / 256, 8192);
+  hipLaunchKernelGGL(linear_reduce_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+int linear_tile_rows() { return BM; }
+int linear_tile_cols() { return BN; }
+int linear_k_tile() { return BK; }
+
+}  // namespace nva

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace nva {
 
 // One unit of the row kernel: one query row attending over the key range [kbeg, kend) of one
@@ -123,6 +125,15 @@ struct NormLaunch {
   int32_t rows, width;
 };
 
+// y[m, n] = x[m, k] w[n, k]^T (+ bias) with K split over `splits` slices of k_per_split.
+struct LinearLaunch {
+  const float *x, *w, *bias;
+  float *y;
+  float *part;  // [splits, m, n] partial sums when splits > 1
+  int32_t m, n, k;
+  int32_t splits, k_per_split;
+};
+
 struct GatherLaunch {
   const float *k_cache, *v_cache;
   float *k_out, *v_out;       // [T, hk, d]
@@ -137,6 +148,10 @@ hipError_t launch_rms_norm(const NormLaunch &a, hipStream_t s);
 size_t rope_store_norm_lds(const RopeStoreLaunch &a);
 constexpr size_t kRopeNormMaxLds = 64 * 1024;
 hipError_t launch_gather(const GatherLaunch &a, hipStream_t s);
+hipError_t launch_linear(const LinearLaunch &a, hipStream_t s);
+int linear_tile_rows();
+int linear_tile_cols();
+int linear_k_tile();
 hipError_t launch_row_attention(const RowLaunch &a, int heads_per_wg, hipStream_t s);
 hipError_t launch_merge(const MergeLaunch &a, hipStream_t s);
 hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream_t s);

@@ -9,6 +9,7 @@ from .layers import (  # noqa: F401
     IllegalArgumentException,
     IllegalStateException,
     KvCacheArena,
+    Linear,
     NullPointerException,
     NvaError,
     RMSNorm,

@@ -126,6 +126,7 @@ SIGNATURES = {
     "nva_rope_attention_forward": ([_vp, _vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci,
                                     _vp, _vp, _vp], _st),
     "nva_rms_norm_forward": ([_vp, _pnorm, _vp, _ci, _ci, _vp], _st),
+    "nva_linear_forward": ([_vp, _vp, _ci, _ci, _vp, _ci, _vp, _vp], _st),
     "nva_build_prefill_metadata": ([_pseq, _ci, _ci, _pmeta], _st),
     "nva_build_decode_metadata": ([_pseq, _ci, _ci, _pmeta], _st),
     "nva_step_prepare_prefill": ([_vp, _pseq, _ci, _ci], _st),

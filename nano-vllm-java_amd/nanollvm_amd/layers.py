@@ -10,6 +10,8 @@ the reference's own code:
 * ``Attention``      -- layers/Attention.java (constructor arguments, ``forward``).
 * ``RMSNorm``        -- layers/Norms.java:32-97 (``forward``; ``weightless``), applied per head
                         by the model layers before RoPE.
+* ``Linear``         -- layers/Linear.java Linear.Row (``forward``): o_proj on the attention
+                        output.
 
 (Reference paths are relative to nano-vllm-java/src/main/java/com/igormaznitsa/nanollvm/.)
 Tensors are torch CUDA float32 tensors (device memory only; torch does no compute here).  Java
@@ -394,6 +396,32 @@ class RMSNorm:
             ctx.handle, self.desc(), _dev(x, "x"), rows, width, _dev(out, "out")),
             "RMSNorm.forward")
         return out
+
+
+class Linear:
+    """Linear.Row(weight [out, in], bias) (layers/Linear.java:296-335): ``forward(x, ctx)`` is
+    Ops.linear, y = x W^T + b, on fp32 MFMA.  ``weight``/``bias`` are float32 device tensors
+    kept resident, as the model's weights are."""
+
+    def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+        if weight.dim() != 2:
+            raise IllegalArgumentException("weight must be 2D")
+        if bias is not None and tuple(bias.shape) != (weight.shape[0],):
+            raise IllegalArgumentException("bias must have out entries")
+        self.weight = weight
+        self.bias = bias
+        self.out_features, self.in_features = weight.shape
+
+    def forward(self, x: torch.Tensor, ctx: "Context") -> torch.Tensor:
+        if x.numel() % self.in_features != 0:
+            raise IllegalArgumentException("x last dim mismatch")
+        rows = x.numel() // self.in_features
+        y = torch.empty(x.shape[:-1] + (self.out_features,) if x.shape[-1] == self.in_features
+                        else (rows, self.out_features), dtype=torch.float32, device=x.device)
+        _check(ctx.handle, N.load().nva_linear_forward(
+            ctx.handle, _dev(x, "x"), rows, self.in_features, _dev(self.weight, "weight"),
+            self.out_features, _dev(self.bias, "bias"), _dev(y, "y")), "Linear.forward")
+        return y
 
 
 class Attention:

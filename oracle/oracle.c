@@ -21,6 +21,10 @@
  *   tensor/vector/VectorFloatKernels.java:57-87,285-317   dot/scale/axpy (kernels mode LANE)
  *   tensor/MatmulRuntime.java:194-225                     parallelRanges (threads > 1)
  *   tensor/Ops.java:444-500         rmsNorm (weightless / weight / onePlusWeight) -> orc_rms_norm()
+ *   tensor/Ops.java:84-124, tensor/MatmulRuntime.java:234-255,396-432   Ops.linear (sequential
+ *                                   runtime) -> orc_linear()
+ *   tensor/scalar/ScalarFloatKernels.java:82-140          gemv / gemvPanel8 (kernels mode 0)
+ *   tensor/vector/VectorFloatKernels.java:158-250         gemv / gemvPanel8 (kernels mode LANE)
  *   tensor/scalar/ScalarFloatKernels.java:45-80           sumSquares/scaleAdd/scaleAddOnePlus
  *   tensor/vector/VectorFloatKernels.java:90-156          sumSquares/scaleAdd/scaleAddOnePlus
  *
@@ -55,6 +59,8 @@
 #define MUT_NORM_DIV_N1 8    /* mean of squares divided by n - 1 */
 #define MUT_NORM_PAIRWISE 9  /* sumSquares summed as a pairwise tree, not in the scalar order */
 #define MUT_NORM_NO_ONE 10   /* onePlusWeight ignored (w instead of 1 + w) */
+#define MUT_LIN_TRANSPOSE 11 /* weight read as [in, out] instead of [out, in] */
+#define MUT_LIN_NO_BIAS 12   /* bias dropped */
 
 typedef struct {
   int num_heads;
@@ -291,6 +297,70 @@ void orc_rms_norm(const float *x, int rows, int width, const float *weight, floa
       o[i] = y;
     }
   }
+}
+
+/* ---------------------------------------------------------------- linear (o_proj) */
+
+/* gemv over outputs [0, out) of one row: panels of 8 outputs, then the tail one by one
+ * (ScalarFloatKernels.gemv / gemvPanel8, ScalarFloatKernels.java:82-140: a_j = bias,
+ * a_j += x_i * w_ji in i order; tail: bias + dot; VectorFloatKernels.java:158-250: per-output
+ * FMA lane accumulators, reduceLanes, scalar tail, then + bias; tail: bias + dot). */
+static void gemv(const float *x, const float *w, const float *bias, float *y, int in, int out,
+                 int mode, int mutation) {
+  const float *b = mutation == MUT_LIN_NO_BIAS ? NULL : bias;
+  float wt[64];
+  int o = 0;
+  for (; o + 8 <= out; o += 8) {
+    if (mode == 0) {
+      float a[8];
+      for (int j = 0; j < 8; j++) a[j] = b ? b[o + j] : 0.0f;
+      for (int i = 0; i < in; i++) {
+        float xv = x[i];
+        for (int j = 0; j < 8; j++) {
+          float wv = mutation == MUT_LIN_TRANSPOSE ? w[(size_t)i * out + o + j]
+                                                   : w[(size_t)(o + j) * in + i];
+          a[j] = a[j] + xv * wv;
+        }
+      }
+      for (int j = 0; j < 8; j++) y[o + j] = a[j];
+    } else {
+      int lane = mode, upper = in - in % lane;
+      for (int j = 0; j < 8; j++) {
+        const float *wr = w + (size_t)(o + j) * in;
+        float acc[16];
+        memset(acc, 0, sizeof(acc));
+        int i = 0;
+        for (; i < upper; i += lane)
+          for (int l = 0; l < lane; l++) acc[l] = fmaf(x[i + l], wr[i + l], acc[l]);
+        for (int l = 0; l < lane; l++) wt[l] = acc[l];
+        for (int half = lane / 2; half >= 1; half /= 2)
+          for (int l = 0; l < half; l++) wt[l] = wt[l] + wt[l + half];
+        float s = wt[0];
+        for (; i < in; i++) s = s + x[i] * wr[i];
+        if (b) s = s + b[o + j];
+        y[o + j] = s;
+      }
+    }
+  }
+  for (; o < out; o++) {
+    float sum = b ? b[o] : 0.0f;
+    const float *wr = w + (size_t)o * in;
+    if (mutation == MUT_LIN_TRANSPOSE) {
+      float d = 0.0f;
+      for (int i = 0; i < in; i++) d = d + x[i] * w[(size_t)i * out + o];
+      y[o] = sum + d;
+    } else {
+      y[o] = sum + dot(x, wr, in, mode);
+    }
+  }
+}
+
+/* Ops.linear(x, weight[out, in], bias) on the sequential runtime: y = x W^T + bias, one gemv per
+ * row (MatmulRuntime.linear -> linearRange / linearDecode1 -> gemv over [0, out)). */
+void orc_linear(const float *x, const float *w, const float *bias, float *y, int rows, int in,
+                int out, int mode, int mutation) {
+  for (int r = 0; r < rows; r++)
+    gemv(x + (size_t)r * in, w, bias, y + (size_t)r * out, in, out, mode, mutation);
 }
 
 /* ---------------------------------------------------------------- store (a2) */

@@ -45,6 +45,11 @@ How each oracle function is pinned (the tests named here live in ``tests/test_or
   :1047-1056 onePlusWeight equals the plain norm times (1 + w); :675 scalar and vector
   sumSquares of 0.1*i agree within 1e-3).  Planted mistakes (no eps, divide by n - 1,
   pairwise order, onePlusWeight ignored) each fail one of them.
+* ``linear`` -- ``tests/test_oracle_linear.py``: against float64 ``x @ W.T + b`` within the
+  first-order bound of a sequential fp32 sum ((in + 1) * 2^-24 * sum|terms|), and the reference's own tests re-expressed (T/CoreUnitTest.java:296-300 identity
+  weight; :432-471 the sequential sum of x[i]*w[o,i] within 1e-4; :473-502 and :705-728 with a
+  bias, scalar vs vector gemv within 1e-4).  Planted mistakes (transposed weight, dropped bias)
+  each fail.
 * ``store_kv`` -- closed form: ``cache[slot] == k[i]`` for slot >= 0, untouched elsewhere.
 
 Not pinned: the exact bits of Java's ``Math.exp`` and of ``FloatVector.reduceLanes`` (the
@@ -83,6 +88,8 @@ MUT_NORM_NO_EPS = 7
 MUT_NORM_DIV_N1 = 8
 MUT_NORM_PAIRWISE = 9
 MUT_NORM_NO_ONE = 10
+MUT_LIN_TRANSPOSE = 11
+MUT_LIN_NO_BIAS = 12
 
 
 class _Attn(ctypes.Structure):
@@ -130,6 +137,8 @@ def lib():
         L.orc_rope_table.restype = None
         L.orc_rope_forward.argtypes = [vp, ci, ci, vp, vp, vp, vp, vp, ci, ci, ci, ci]
         L.orc_rope_forward.restype = ci
+        L.orc_linear.argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci]
+        L.orc_linear.restype = None
         L.orc_sum_squares.argtypes = [vp, ci, ci, ci]
         L.orc_sum_squares.restype = cf
         L.orc_rms_norm.argtypes = [vp, ci, ci, vp, cf, ci, ci, ci, vp]
@@ -235,6 +244,21 @@ def rms_norm_fp64(x, weight=None, eps: float = 1e-6, one_plus: bool = False) -> 
     if weight is not None:
         w = np.asarray(weight, np.float64)
         y = y * (1.0 + w if one_plus else w)
+    return y
+
+
+# ---------------------------------------------------------------------------------------- linear
+
+def linear(x, weight, bias=None, mode: int = 0, mutation: int = MUT_NONE) -> np.ndarray:
+    """Ops.linear(x, weight [out, in], bias) on the sequential runtime: x @ weight.T + bias,
+    with the scalar (mode 0) or Vector API (8 / 16 lanes) gemv order."""
+    x = _f32(x)
+    w = _f32(weight)
+    out_f, in_f = w.shape
+    rows = x.size // in_f
+    b = None if bias is None else _f32(bias)
+    y = np.zeros(x.shape[:-1] + (out_f,), np.float32)
+    lib().orc_linear(_p(x), _p(w), _p(b), _p(y), rows, in_f, out_f, int(mode), int(mutation))
     return y
 
 

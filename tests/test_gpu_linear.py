@@ -1,0 +1,93 @@
+"""o_proj (Linear.Row -> Ops.linear) on fp32 MFMA through the C ABI, against the oracle's
+restatement of the reference's gemv at decode shapes, and against float64 at the full prefill
+shapes.  Bar: max-abs 1e-4 and rel-L2 1e-5, the path's floating-point tolerance."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from cases import rel_l2
+from nanollvm_amd import Context, Linear, UnsupportedShapeError
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 1e-4
+REL_L2 = 1e-5
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def data(rows, inf, outf, bias, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, inf)).astype(np.float32)
+    w = (rng.standard_normal((outf, inf)) / np.sqrt(inf)).astype(np.float32)
+    b = rng.standard_normal(outf).astype(np.float32) if bias else None
+    return x, w, b
+
+
+def run(ctx, x, w, b):
+    lin = Linear(dev(w), None if b is None else dev(b))
+    y = lin.forward(dev(x), ctx)
+    ctx.sync()
+    return y.cpu().numpy()
+
+
+def check(got, want, name):
+    err = float(np.max(np.abs(got - want)))
+    rl2 = rel_l2(got, want)
+    say(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+    assert np.all(np.isfinite(got))
+    assert err <= MAX_ABS and rl2 <= REL_L2, (err, rl2)
+
+
+@pytest.mark.parametrize("rows,inf,outf,bias", [
+    (1, 2048, 1024, False),    # one decode row, Qwen3-0.6B o_proj
+    (8, 2048, 1024, True),     # 8-row decode batch
+    (37, 260, 200, True),      # ragged M, N, K (K % 32 != 0)
+    (130, 2048, 1024, False),  # M tail past one 128-row tile
+    (256, 2048, 1024, True),   # 256-row decode batch
+])
+def test_linear_matches_oracle(ctx, rows, inf, outf, bias):
+    x, w, b = data(rows, inf, outf, bias, rows + inf)
+    check(run(ctx, x, w, b), O.linear(x, w, b), f"linear {rows}x{inf}->{outf} bias={bias}")
+
+
+@pytest.mark.parametrize("rows,inf,outf", [(4096, 2048, 1024), (512, 4096, 2560)])
+def test_linear_full_prefill_shapes_fp64(ctx, rows, inf, outf):
+    """Qwen3-0.6B o_proj over the 4096-token prefill, and a Qwen3-4B-like o_proj."""
+    x, w, b = data(rows, inf, outf, True, 3)
+    want = x.astype(np.float64) @ w.astype(np.float64).T + b
+    check(run(ctx, x, w, b), want, f"linear {rows}x{inf}->{outf} vs fp64")
+
+
+def test_reference_linear_cases(ctx):
+    # T/CoreUnitTest.java:296-300 (identity) and :432-471 (rows 4, in 64, out 32)
+    y = run(ctx, np.array([[2.0, 3.0, 0.0, 0.0]], np.float32),
+            np.array([[1, 0, 0, 0], [0, 1, 0, 0]], np.float32), None)
+    assert abs(y[0, 0] - 2.0) < 1e-5 and abs(y[0, 1] - 3.0) < 1e-5
+    x = ((np.arange(4 * 64) % 7) * np.float32(0.1)).astype(np.float32).reshape(4, 64)
+    w = (((np.arange(32 * 64) * 3) % 11) * np.float32(0.05)).astype(np.float32).reshape(32, 64)
+    assert np.max(np.abs(run(ctx, x, w, None) - O.linear(x, w))) <= 1e-4
+
+
+def test_linear_rejects_unaligned_width(ctx):
+    x, w, _ = data(3, 6, 5, False, 1)
+    with pytest.raises(UnsupportedShapeError):
+        run(ctx, x, w, None)
