@@ -44,6 +44,12 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work budget of the baseline")
     ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    ap.add_argument("--workload", choices=sorted(EXTRA), default=None,
+                    help="measure one more workload instead of the headline pair and print its "
+                         "own JSON line")
+    ap.add_argument("--flush", action="store_true",
+                    help="write 512 MB between steps so K/V that fits the 256 MB Infinity Cache "
+                         "is read from HBM (kernel timings exclude the flush)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy three times (the "
                          "known-size reference for the FETCH_SIZE/WRITE_SIZE counters)")
@@ -137,7 +143,8 @@ def kernel_a_bytes(wl, k_out):
                 4 * d * 2 * hkv + 4 * d + 8)
 
 
-def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, label):
+def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, label,
+              flush=None):
     import torch
     from nanollvm_amd import Context  # noqa: F401
 
@@ -158,6 +165,8 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
+        if flush is not None:
+            flush()
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -200,6 +209,38 @@ def time_step_prepare(ctx, wl, reps=30):
     upload = 4 * (tokens * 2 + bt + 2 * (len(wl.seqs) + 1) + len(wl.seqs))
     return {"build_upload_us": round((t1 - t0) / reps * 1e6, 1), "sequences": len(wl.seqs),
             "tokens": tokens, "pages": pages, "upload_bytes": upload}
+
+
+def time_o_proj(ctx, attn_out, wl, steps, warmup, hidden=1024, seed=21):
+    """o_proj (Linear.Row, Qwen3-0.6B: [hidden, Hq * d] weight) on this step's attention output,
+    timed like the step.  Reported beside the step, not inside its value."""
+    import torch
+    from nanollvm_amd import Linear
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    k = wl.hq * wl.d
+    w = torch.randn((hidden, k), device="cuda", generator=g) / math.sqrt(k)
+    lin = Linear(w)
+    x = attn_out.reshape(attn_out.shape[0], k)
+    for _ in range(warmup):
+        lin.forward(x, ctx)
+    torch.cuda.synchronize()
+    ctx.reset_stats()
+    ctx.set_timing(True)
+    for _ in range(steps):
+        lin.forward(x, ctx)
+    torch.cuda.synchronize()
+    ctx.set_timing(False)
+    n, t = ctx.kernel_stats("linear")
+    ms = t / max(n, 1)
+    m = x.shape[0]
+    flops = 2.0 * m * hidden * k
+    byts = 4.0 * (m * k + hidden * k + m * hidden)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"kernel": "linear_kernel (fp32 MFMA 32x32x2, split-K + reduce when few rows)",
+            "shape": f"[{m}, {k}] x [{hidden}, {k}]^T", "ms": round(ms, 5),
+            "tflops": round(tf, 2), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}
 
 
 def kernel_a_roofline(wl, stats):
@@ -249,6 +290,10 @@ def bench_decode(args, ctx):
         "kernel_a": kernel_a_roofline(wl, stats),
         "step_metadata": time_step_prepare(ctx, wl),
     }
+    ctx.set(**wl.meta.context_args())
+    ctx.bind_kv_cache(arena)
+    res["o_proj"] = time_o_proj(ctx, attn.forward_with_rope(rope, wl.meta.positions, q, k, v, ctx),
+                                wl, args.steps, args.warmup)
     rope.close()
     arena.close()
     return res
@@ -292,9 +337,85 @@ def bench_prefill(args, ctx):
         "kernel_a": kernel_a_roofline(wl, stats),
         "step_metadata": time_step_prepare(ctx, wl),
     }
+    ctx.set(**wl.meta.context_args())
+    ctx.bind_kv_cache(arena)
+    res["o_proj"] = time_o_proj(ctx, attn.forward_with_rope(rope, wl.meta.positions, q, k, v, ctx),
+                                wl, args.steps, args.warmup)
     rope.close()
     arena.close()
     return res
+
+
+# Other workloads of the path, measured one per run with --workload (each prints its own line).
+def _extra_builders():
+    from nanollvm_amd import workloads as W
+    return {
+        "c1-qwen3-decode-b8": W.qwen3_decode_small,
+        "c3-gemma3-decode-local": lambda: W.gemma3_decode(local=True),
+        "c3-gemma3-decode-global": lambda: W.gemma3_decode(local=False),
+        "c5-qwen3-4b-mixed": W.qwen3_4b_mixed,
+    }
+
+
+EXTRA = ["c1-qwen3-decode-b8", "c3-gemma3-decode-local", "c3-gemma3-decode-global",
+         "c5-qwen3-4b-mixed"]
+
+
+def bench_extra(args, ctx):
+    """One workload's step: per-kernel times, the decode rows' GB/s over the row kernel, the
+    prefill rows' TFLOP/s over the MFMA kernel, and the step's lower bound at peak
+    (max of HBM bytes / 8 TB/s and MFMA flops / 157.3 TFLOP/s)."""
+    import numpy as np
+    import torch
+    from nanollvm_amd import Attention, KvCacheArena, RotaryEmbedding
+
+    wl = _extra_builders()[args.workload]()
+    log(f"workload: {wl.name}: {len(wl.seqs)} seqs, {wl.tokens} new tokens, {wl.num_blocks} blocks")
+    arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+    fill_arena_normal(arena, 0, 4321)
+    rope = RotaryEmbedding(ctx, wl.d, wl.d, wl.max_pos, wl.rope_theta)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    T = wl.tokens
+    q = torch.randn((T, wl.hq, wl.d), device="cuda", generator=g)
+    k = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
+    v = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
+    oq = torch.empty_like(q)
+    attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
+    junk = torch.empty(512 << 18, device="cuda") if args.flush else None
+    flush = (lambda: junk.fill_(1.0)) if args.flush else None
+    ms, stats = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps, args.warmup,
+                          wl.name, flush=flush)
+    dec_rows = [(c, n) for c, n in wl.seqs if n == 1]
+    pf_rows = [(c, n) for c, n in wl.seqs if n > 1]
+    dec_bytes = 0
+    for c, _ in dec_rows:
+        vis = min(c + 1, wl.window) if wl.window > 0 else c + 1
+        dec_bytes += vis * wl.hkv * wl.d * 8 + wl.hq * wl.d * 8 + 4 * (-(-(c + 1) // wl.block_size) + 1)
+    pairs = 0
+    for c, n in pf_rows:
+        kk = np.arange(c + 1, c + n + 1, dtype=np.int64)
+        pairs += int(np.minimum(kk, wl.window).sum() if wl.window > 0 else kk.sum())
+    flops = 4.0 * wl.d * wl.hq * pairs
+    kms = {n: s[1] / max(s[0], 1) for n, s in stats.items() if s[0]}
+    line = {"workload": wl.name, "ms_per_step": round(ms, 5),
+            "kernel_ms": {n: round(x, 5) for n, x in kms.items()}, "flush": bool(args.flush),
+            "dtype": "f32", "data": "synthetic (seeded N(0,1) q/k/v and pages)"}
+    if dec_rows and "decode" in kms:
+        gbs = dec_bytes / (kms["decode"] * 1e-3) / 1e9
+        line["decode_rows"] = {"rows": len(dec_rows), "bytes": dec_bytes, "gbs": round(gbs, 1),
+                               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if pf_rows and "prefill" in kms:
+        tf = flops / (kms["prefill"] * 1e-3) / 1e12
+        line["prefill_rows"] = {"tokens": int(sum(n for _, n in pf_rows)), "flops": flops,
+                                "tflops": round(tf, 2),
+                                "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+    bound = max(dec_bytes / (HBM_PEAK_GBS * 1e9), flops / (FP32_MFMA_PEAK_TFLOPS * 1e12)) * 1e3
+    line["lower_bound_ms"] = round(bound, 5)
+    line["attention_ms"] = round(sum(kms.get(n, 0.0) for n in ("decode", "prefill", "merge")), 5)
+    rope.close()
+    arena.close()
+    return line
 
 
 def cpu_baseline(wl, budget_s):
@@ -370,6 +491,11 @@ def main():
 
     torch.cuda.init()
     ctx = Context(0)
+    if args.workload:
+        line = bench_extra(args, ctx)
+        ctx.close()
+        print(json.dumps(line), flush=True)
+        return
     dec = pf = None
     if args.only in (None, "decode"):
         dec = bench_decode(args, ctx)
@@ -398,6 +524,7 @@ def main():
             "roofline": dec["roofline"],
             "kernel_a": dec["kernel_a"],
             "step_metadata": dec["step_metadata"],
+            "o_proj": dec["o_proj"],
         })
     else:
         line.update({"value": pf["tflops"], "unit": "TFLOP/s", "ms_per_step": pf["ms_per_step"],

@@ -120,6 +120,7 @@ struct Plan {
   bool valid = false;
   int num_rows = 0, num_merge = 0, num_tiles = 0, num_parts = 0;
   int num_slots = 0;  // prefill stream-K slots (grid x)
+  int max_parts = 0;  // most partials any merged row has
   bool covers_all = true;  // every output row is written by some kernel
   size_t off_rows = 0, off_merge = 0, off_tiles = 0, off_slots = 0;
   DevBuf dev;
@@ -142,6 +143,8 @@ struct nva_ctx {
   int device = 0;
   int num_cus = 256;
   hipStream_t own_stream = nullptr;
+  hipStream_t side_stream = nullptr;  // decode rows of a mixed step run here, beside the tiles
+  hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   hipStream_t stream = nullptr;
   std::string err;
 
@@ -235,18 +238,20 @@ hipEvent_t take_event(nva_ctx *ctx) {
 struct Timed {
   nva_ctx *ctx;
   const char *name;
+  hipStream_t stream;
   hipEvent_t start = nullptr;
-  Timed(nva_ctx *c, const char *n) : ctx(c), name(n) {
+  Timed(nva_ctx *c, const char *n, hipStream_t s = nullptr)
+      : ctx(c), name(n), stream(s ? s : c->stream) {
     if (ctx->timing) {
       start = take_event(ctx);
-      if (start) (void)hipEventRecord(start, ctx->stream);
+      if (start) (void)hipEventRecord(start, stream);
     }
   }
   void done() {
     if (!start) return;
     hipEvent_t stop = take_event(ctx);
     if (!stop) return;
-    (void)hipEventRecord(stop, ctx->stream);
+    (void)hipEventRecord(stop, stream);
     ctx->pending.push_back({name, start, stop});
     start = nullptr;
   }
@@ -494,6 +499,8 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   plan->num_tiles = (int)tiles.size();
   plan->num_parts = parts;
   plan->num_slots = slots;
+  plan->max_parts = 0;
+  for (const MergeItem &mi : merges) plan->max_parts = std::max(plan->max_parts, mi.nparts);
   plan->off_rows = 0;
   plan->off_merge = plan->off_rows + items.size() * sizeof(RowItem);
   plan->off_tiles = plan->off_merge + merges.size() * sizeof(MergeItem);
@@ -577,6 +584,35 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     HIP_TRY(ctx, ctx->d_part.reserve(need), "partial buffer");
   }
   float *pm = static_cast<float *>(ctx->d_part.ptr);
+  // A mixed step (MFMA tiles and rows in one plan) runs the HBM-bound rows on the side stream
+  // while the MFMA-bound tiles run on the main stream; both write disjoint partials, and the
+  // main stream waits for the side stream before the merge.
+  const bool fork = plan->num_tiles > 0 && plan->num_rows > 0;
+  hipStream_t row_stream = ctx->stream;
+  if (fork) {
+    HIP_TRY(ctx, hipEventRecord(ctx->fork_ev, ctx->stream), "fork record");
+    HIP_TRY(ctx, hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0), "fork wait");
+    row_stream = ctx->side_stream;
+  }
+  if (plan->num_rows > 0) {
+    RowLaunch r;
+    r.q = q;
+    r.out = out;
+    r.kv = view;
+    r.items = reinterpret_cast<const RowItem *>(pbase + plan->off_rows);
+    r.num_items = plan->num_rows;
+    r.hq = d.num_heads;
+    r.hkv = d.num_kv_heads;
+    r.head_dim = d.head_dim;
+    r.scale = d.scale;
+    r.part_m = pm;
+    r.part_l = pm + parts;
+    r.part_acc = pm + 2 * parts;
+    Timed tm(ctx, "decode", row_stream);
+    HIP_TRY(ctx, launch_row_attention(r, hpw_row, row_stream), "decode kernel launch");
+    tm.done();
+  }
+  if (fork) HIP_TRY(ctx, hipEventRecord(ctx->join_ev, ctx->side_stream), "join record");
   if (plan->num_tiles > 0) {
     TileLaunch t;
     t.q = q;
@@ -598,24 +634,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     HIP_TRY(ctx, launch_prefill_tiles(t, hpw_tile, ctx->stream), "prefill kernel launch");
     tm.done();
   }
-  if (plan->num_rows > 0) {
-    RowLaunch r;
-    r.q = q;
-    r.out = out;
-    r.kv = view;
-    r.items = reinterpret_cast<const RowItem *>(pbase + plan->off_rows);
-    r.num_items = plan->num_rows;
-    r.hq = d.num_heads;
-    r.hkv = d.num_kv_heads;
-    r.head_dim = d.head_dim;
-    r.scale = d.scale;
-    r.part_m = pm;
-    r.part_l = pm + parts;
-    r.part_acc = pm + 2 * parts;
-    Timed tm(ctx, "decode");
-    HIP_TRY(ctx, launch_row_attention(r, hpw_row, ctx->stream), "decode kernel launch");
-    tm.done();
-  }
+  if (fork) HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0), "join wait");
   if (plan->num_merge > 0) {
     MergeLaunch mg;
     mg.out = out;
@@ -627,7 +646,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     mg.part_l = pm + parts;
     mg.part_acc = pm + 2 * parts;
     Timed tm(ctx, "merge");
-    HIP_TRY(ctx, launch_merge(mg, ctx->stream), "merge kernel launch");
+    HIP_TRY(ctx, launch_merge(mg, plan->max_parts, ctx->stream), "merge kernel launch");
     tm.done();
   }
   return NVA_OK;
@@ -800,7 +819,14 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
     ctx->num_cus = prop.multiProcessorCount;
-  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
+  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess) {
+    if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
+    if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+    if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return NVA_E_HIP;
   }
@@ -813,6 +839,7 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   if (!ctx) return NVA_OK;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamSynchronize(ctx->side_stream);
   resolve_timings(ctx);
   for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
   for (Plan *p : ctx->plans) {
@@ -828,6 +855,9 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   ctx->d_v_norm.release();
   ctx->d_lin.release();
   ctx->d_gather.release();
+  (void)hipEventDestroy(ctx->fork_ev);
+  (void)hipEventDestroy(ctx->join_ev);
+  (void)hipStreamDestroy(ctx->side_stream);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
   return NVA_OK;

@@ -230,8 +230,9 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   }
 }
 
-// Log-sum-exp merge of the chunk partials of split rows; rows with no visible key get zeros.
-__global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
+// Row-wide merge for plans whose split rows have few partials (prefill segments): one workgroup
+// per row covers all heads, each thread folding the partials of one float4 of one head in order.
+__global__ void __launch_bounds__(256) merge_rows_kernel(MergeLaunch a) {
   const MergeItem it = a.items[blockIdx.x];
   const int d4 = a.head_dim >> 2;
   for (int idx = threadIdx.x; idx < a.hq * d4; idx += blockDim.x) {
@@ -258,6 +259,87 @@ __global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
       r = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
     }
     st4(a.out + ((size_t)it.qrow * a.hq + h) * a.head_dim + cc * 4, r);
+  }
+}
+
+// Log-sum-exp merge of the chunk partials of split rows; rows with no visible key get zeros.
+// One workgroup per (row, head): wave w folds partials w, w + 4, ... (four loads in flight per
+// lane), lane c holding float4 c (and c + 64 at d = 512) of the head; the four waves' (m, l, acc)
+// are then combined in wave order through LDS, so the result is deterministic.
+__global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
+  __shared__ float sm[4], sl[4];
+  __shared__ float4 sacc[4][128];
+  const MergeItem it = a.items[blockIdx.x];
+  const int h = blockIdx.y;
+  const int d4 = a.head_dim >> 2;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  float4 *out = reinterpret_cast<float4 *>(a.out + ((size_t)it.qrow * a.hq + h) * a.head_dim);
+  if (it.nparts <= 0) {
+    for (int c = threadIdx.x; c < d4; c += blockDim.x) out[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    return;
+  }
+  // Pass 1: this wave's max over its partials.
+  float M = -INFINITY;
+  for (int p = wave; p < it.nparts; p += 4)
+    M = fmaxf(M, a.part_m[(size_t)(it.first + p) * a.hq + h]);
+  const float Ms = M == -INFINITY ? 0.0f : M;
+  float L = 0.0f;
+  float4 A0 = make_float4(0.f, 0.f, 0.f, 0.f), A1 = A0;
+  const bool c0 = lane < d4, c1 = lane + 64 < d4;
+  for (int p0 = wave; p0 < it.nparts; p0 += 16) {
+    float e[4];
+    float4 x0[4], x1[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int p = p0 + 4 * u;
+      const bool ok = p < it.nparts;
+      const size_t pi = (size_t)(it.first + (ok ? p : p0)) * a.hq + h;
+      e[u] = ok ? __builtin_amdgcn_exp2f(a.part_m[pi] - Ms) : 0.0f;
+      L = fmaf(ok ? a.part_l[pi] : 0.0f, e[u], L);
+      const float4 *src = reinterpret_cast<const float4 *>(a.part_acc + pi * a.head_dim);
+      x0[u] = c0 ? src[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+      x1[u] = c1 ? src[lane + 64] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      A0.x = fmaf(x0[u].x, e[u], A0.x);
+      A0.y = fmaf(x0[u].y, e[u], A0.y);
+      A0.z = fmaf(x0[u].z, e[u], A0.z);
+      A0.w = fmaf(x0[u].w, e[u], A0.w);
+      A1.x = fmaf(x1[u].x, e[u], A1.x);
+      A1.y = fmaf(x1[u].y, e[u], A1.y);
+      A1.z = fmaf(x1[u].z, e[u], A1.z);
+      A1.w = fmaf(x1[u].w, e[u], A1.w);
+    }
+  }
+  if (lane == 0) {
+    sm[wave] = M;
+    sl[wave] = L;
+  }
+  if (c0) sacc[wave][lane] = A0;
+  if (c1) sacc[wave][lane + 64] = A1;
+  __syncthreads();
+  float G = -INFINITY;
+  for (int w = 0; w < 4; w++) G = fmaxf(G, sm[w]);
+  const float Gs = G == -INFINITY ? 0.0f : G;
+  float ew[4];
+  float LT = 0.0f;
+  for (int w = 0; w < 4; w++) {
+    ew[w] = __builtin_amdgcn_exp2f(sm[w] - Gs);
+    LT = fmaf(sl[w], ew[w], LT);
+  }
+  const float inv = LT == 0.0f ? 0.0f : 1.0f / LT;
+  for (int c = threadIdx.x; c < d4; c += blockDim.x) {
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int w = 0; w < 4; w++) {
+      const float4 x = sacc[w][c];
+      r.x = fmaf(x.x, ew[w], r.x);
+      r.y = fmaf(x.y, ew[w], r.y);
+      r.z = fmaf(x.z, ew[w], r.z);
+      r.w = fmaf(x.w, ew[w], r.w);
+    }
+    out[c] = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
   }
 }
 
@@ -308,9 +390,14 @@ hipError_t launch_row_attention(const RowLaunch &a, int hpw, hipStream_t s) {
   }
 }
 
-hipError_t launch_merge(const MergeLaunch &a, hipStream_t s) {
+hipError_t launch_merge(const MergeLaunch &a, int max_parts, hipStream_t s) {
   if (a.num_items <= 0) return hipSuccess;
-  hipLaunchKernelGGL(merge_kernel, dim3(a.num_items), dim3(256), 0, s, a);
+  if (a.head_dim > 512 || (a.head_dim & 3)) return hipErrorInvalidValue;
+  // Few partials per row: one row-wide workgroup per row; many: spread them over waves.
+  if (max_parts <= 4)
+    hipLaunchKernelGGL(merge_rows_kernel, dim3(a.num_items), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(merge_kernel, dim3(a.num_items, a.hq), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

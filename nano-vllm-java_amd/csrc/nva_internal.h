@@ -153,7 +153,7 @@ int linear_tile_rows();
 int linear_tile_cols();
 int linear_k_tile();
 hipError_t launch_row_attention(const RowLaunch &a, int heads_per_wg, hipStream_t s);
-hipError_t launch_merge(const MergeLaunch &a, hipStream_t s);
+hipError_t launch_merge(const MergeLaunch &a, int max_parts, hipStream_t s);
 hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream_t s);
 
 // Shapes the kernels are instantiated for.
