@@ -479,14 +479,15 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
       merges.push_back({r.qrow, 0, 0, 0});
       continue;
     }
-    if (len <= chunk) {
+    const int rchunk = chunk;
+    if (len <= rchunk) {
       items.push_back({r.qrow, r.seq, r.kbase, r.kbeg, r.kend, -1, 0, 0});
       continue;
     }
-    const int n = (len + chunk - 1) / chunk;
+    const int n = (len + rchunk - 1) / rchunk;
     for (int j = 0; j < n; j++) {
-      const int b0 = r.kbeg + j * chunk;
-      const int b1 = std::min(r.kend, b0 + chunk);
+      const int b0 = r.kbeg + j * rchunk;
+      const int b1 = std::min(r.kend, b0 + rchunk);
       items.push_back({r.qrow, r.seq, r.kbase, b0, b1, parts + j, 0, 0});
     }
     merges.push_back({r.qrow, parts, n, 0});

@@ -263,12 +263,13 @@ __global__ void __launch_bounds__(256) merge_rows_kernel(MergeLaunch a) {
 }
 
 // Log-sum-exp merge of the chunk partials of split rows; rows with no visible key get zeros.
-// One workgroup per (row, head): wave w folds partials w, w + 4, ... (four loads in flight per
-// lane), lane c holding float4 c (and c + 64 at d = 512) of the head; the four waves' (m, l, acc)
-// are then combined in wave order through LDS, so the result is deterministic.
-__global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
-  __shared__ float sm[4], sl[4];
-  __shared__ float4 sacc[4][128];
+// One workgroup of NW waves per (row, head): wave w folds partials w, w + NW, ... (four loads in
+// flight per lane), lane c holding float4 c (and c + 64 at d = 512) of the head; the waves'
+// (m, l, acc) are then combined in wave order through LDS, so the result is deterministic.
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) merge_kernel(MergeLaunch a) {
+  __shared__ float sm[NW], sl[NW];
+  __shared__ float4 sacc[NW][128];
   const MergeItem it = a.items[blockIdx.x];
   const int h = blockIdx.y;
   const int d4 = a.head_dim >> 2;
@@ -281,18 +282,18 @@ __global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
   }
   // Pass 1: this wave's max over its partials.
   float M = -INFINITY;
-  for (int p = wave; p < it.nparts; p += 4)
+  for (int p = wave; p < it.nparts; p += NW)
     M = fmaxf(M, a.part_m[(size_t)(it.first + p) * a.hq + h]);
   const float Ms = M == -INFINITY ? 0.0f : M;
   float L = 0.0f;
   float4 A0 = make_float4(0.f, 0.f, 0.f, 0.f), A1 = A0;
   const bool c0 = lane < d4, c1 = lane + 64 < d4;
-  for (int p0 = wave; p0 < it.nparts; p0 += 16) {
+  for (int p0 = wave; p0 < it.nparts; p0 += 4 * NW) {
     float e[4];
     float4 x0[4], x1[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int p = p0 + 4 * u;
+      const int p = p0 + NW * u;
       const bool ok = p < it.nparts;
       const size_t pi = (size_t)(it.first + (ok ? p : p0)) * a.hq + h;
       e[u] = ok ? __builtin_amdgcn_exp2f(a.part_m[pi] - Ms) : 0.0f;
@@ -321,23 +322,20 @@ __global__ void __launch_bounds__(256) merge_kernel(MergeLaunch a) {
   if (c1) sacc[wave][lane + 64] = A1;
   __syncthreads();
   float G = -INFINITY;
-  for (int w = 0; w < 4; w++) G = fmaxf(G, sm[w]);
+  for (int w = 0; w < NW; w++) G = fmaxf(G, sm[w]);
   const float Gs = G == -INFINITY ? 0.0f : G;
-  float ew[4];
   float LT = 0.0f;
-  for (int w = 0; w < 4; w++) {
-    ew[w] = __builtin_amdgcn_exp2f(sm[w] - Gs);
-    LT = fmaf(sl[w], ew[w], LT);
-  }
+  for (int w = 0; w < NW; w++) LT = fmaf(sl[w], __builtin_amdgcn_exp2f(sm[w] - Gs), LT);
   const float inv = LT == 0.0f ? 0.0f : 1.0f / LT;
   for (int c = threadIdx.x; c < d4; c += blockDim.x) {
     float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int w = 0; w < 4; w++) {
+    for (int w = 0; w < NW; w++) {
+      const float ew = __builtin_amdgcn_exp2f(sm[w] - Gs);
       const float4 x = sacc[w][c];
-      r.x = fmaf(x.x, ew[w], r.x);
-      r.y = fmaf(x.y, ew[w], r.y);
-      r.z = fmaf(x.z, ew[w], r.z);
-      r.w = fmaf(x.w, ew[w], r.w);
+      r.x = fmaf(x.x, ew, r.x);
+      r.y = fmaf(x.y, ew, r.y);
+      r.z = fmaf(x.z, ew, r.z);
+      r.w = fmaf(x.w, ew, r.w);
     }
     out[c] = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
   }
@@ -393,11 +391,13 @@ hipError_t launch_row_attention(const RowLaunch &a, int hpw, hipStream_t s) {
 hipError_t launch_merge(const MergeLaunch &a, int max_parts, hipStream_t s) {
   if (a.num_items <= 0) return hipSuccess;
   if (a.head_dim > 512 || (a.head_dim & 3)) return hipErrorInvalidValue;
-  // Few partials per row: one row-wide workgroup per row; many: spread them over waves.
+  // Few partials per row: one row-wide workgroup per row; many: spread them over 4 or 16 waves.
   if (max_parts <= 4)
     hipLaunchKernelGGL(merge_rows_kernel, dim3(a.num_items), dim3(256), 0, s, a);
+  else if (max_parts <= 32)
+    hipLaunchKernelGGL((merge_kernel<4>), dim3(a.num_items, a.hq), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(merge_kernel, dim3(a.num_items, a.hq), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((merge_kernel<16>), dim3(a.num_items, a.hq), dim3(1024), 0, s, a);
   return hipGetLastError();
 }
 
