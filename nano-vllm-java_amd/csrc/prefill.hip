@@ -322,7 +322,7 @@ hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
 }  // namespace
 
 bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
-  return (head_dim == 64 || head_dim == 128) &&
+  return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
          (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8);
 }
 
@@ -355,7 +355,9 @@ int blocks_per_cu_d(int hpw) {
 }  // namespace
 
 int prefill_blocks_per_cu(int head_dim, int heads_per_wg) {
-  return head_dim == 64 ? blocks_per_cu_d<64>(heads_per_wg) : blocks_per_cu_d<128>(heads_per_wg);
+  if (head_dim == 64) return blocks_per_cu_d<64>(heads_per_wg);
+  if (head_dim == 256) return blocks_per_cu_d<256>(heads_per_wg);
+  return blocks_per_cu_d<128>(heads_per_wg);
 }
 
 hipError_t launch_prefill_tiles(const TileLaunch &a, int hpw, hipStream_t s) {
@@ -363,6 +365,7 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int hpw, hipStream_t s) {
   switch (a.head_dim) {
     case 64: return launch_prefill_d<64>(a, hpw, s);
     case 128: return launch_prefill_d<128>(a, hpw, s);
+    case 256: return launch_prefill_d<256>(a, hpw, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -16,6 +16,7 @@ Named workloads (q heads / kv heads / head dim):
                           1024 tokens (4 full pages) cached, RoPE theta 1e6, 16/8/128.
 * ``gemma3_decode``       Gemma3-270M decode, 32 seqs, ctx log-U[512,8192], 4/1/256, scale
                           1/16, local layer window 512 or global layer.
+* ``gemma3_prefill``      Gemma3-270M varlen prefill 512/1024/1536/2048, 4/1/256, local or global.
 * ``qwen3_decode_large``  Qwen3-0.6B shape decode, 256 seqs, ctx log-U[128,32768].
 * ``qwen3_4b_mixed``      Qwen3-4B-like mixed step, 32/8/128: 4 prefill chunks of 512 tokens
                           with prior context U[0,4096] plus 64 decode rows (qLen 1) with ctx
@@ -164,6 +165,15 @@ def gemma3_decode(seed=0, local=True) -> Workload:
     return build(f"gemma3-270m decode B=32 ctx log-U[512,8192] {'local W=512' if local else 'global'}",
                  [(c - 1, 1) for c in ctx], is_prefill=False, hq=4, hkv=1, d=256,
                  scale=GEMMA_SCALE, window=512 if local else 0, rng=rng,
+                 rope_theta=1e4 if local else 1e6, max_pos=32768)
+
+
+def gemma3_prefill(seed=0, local=True) -> Workload:
+    """Gemma3-270M-shaped varlen prefill 512/1024/1536/2048 (no cached prefix), 4/1/256."""
+    rng = np.random.default_rng(seed)
+    return build(f"gemma3-270m varlen prefill 512/1024/1536/2048 {'local W=512' if local else 'global'}",
+                 [(0, 512), (0, 1024), (0, 1536), (0, 2048)], is_prefill=True, hq=4, hkv=1,
+                 d=256, scale=GEMMA_SCALE, window=512 if local else 0, rng=rng,
                  rope_theta=1e4 if local else 1e6, max_pos=32768)
 
 

@@ -219,3 +219,14 @@ def test_qwen3_4b_mixed_reduced_contexts(ctx):
     reduced 4-8x so the CPU oracle finishes in seconds."""
     wl = W.qwen3_4b_mixed(chunks=4, chunk=256, prior_hi=1024, rows=16, ctx_lo=512, ctx_hi=2048)
     check_attention(ctx, Case(wl, seed=0), "qwen3-4b mixed (reduced)")
+
+
+@pytest.mark.parametrize("hq,window", [(4, 512), (4, 0), (8, 512)])
+def test_gemma_prefill_d256_mfma(ctx, hq, window):
+    """Gemma-shaped varlen prefill on the MFMA kernel at head_dim 256 (Gemma3-270M: 4 q heads /
+    1 kv head; Gemma 4 sliding layers: 8 / 1), scale 1/16, with a prefix-cache hit, a mid-page
+    chunk start and sequences longer than the 512-token window."""
+    rng = np.random.default_rng(17 + hq + window)
+    wl = W.build("gemma prefill d256", [(0, 700), (512, 300), (37, 129)], is_prefill=True,
+                 hq=hq, hkv=1, d=256, scale=W.GEMMA_SCALE, window=window, rng=rng)
+    check_attention(ctx, Case(wl, seed=5), f"gemma prefill d=256 hq={hq} W={window}")
