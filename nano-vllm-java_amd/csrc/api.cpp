@@ -104,13 +104,14 @@ struct Staging {
 // configuration.
 struct PlanKey {
   int window, mfma, tile_q, wg_per_item, blocks_per_cu;
+  int tile_groups;             // prefill grid height: KV heads x query-head groups
   int tokens;                  // rows of q / out in the forward call
   int paged;                   // keys through block tables (else dense k/v rows)
   int block_size, num_blocks;  // arena geometry the tables are checked against
   bool operator==(const PlanKey &o) const {
     return window == o.window && mfma == o.mfma && tile_q == o.tile_q &&
            wg_per_item == o.wg_per_item && blocks_per_cu == o.blocks_per_cu &&
-           tokens == o.tokens && paged == o.paged &&
+           tile_groups == o.tile_groups && tokens == o.tokens && paged == o.paged &&
            block_size == o.block_size && num_blocks == o.num_blocks;
   }
 };
@@ -406,7 +407,7 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     int64_t total = 0;
     for (const TileItem &t : tiles) total += (t.ke - t.ks + KT - 1) / KT;
     const int64_t resident = (int64_t)ctx->num_cus * key.blocks_per_cu;
-    slots = (int)std::max<int64_t>(1, std::min<int64_t>(total, resident / key.wg_per_item));
+    slots = (int)std::max<int64_t>(1, std::min<int64_t>(total, resident / key.tile_groups));
     const int64_t page_cap =
         paged ? (int64_t)(kPrefillTablePages - 2) * key.block_size / KT * KT : INT32_MAX;
     std::vector<std::vector<TileItem>> per_slot(slots);
@@ -553,7 +554,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
                          int num_blocks, const float *q, int num_tokens, float *out) {
   const int rep = d.num_heads / d.num_kv_heads;
   const int hpw_row = largest_pow2_divisor_upto(rep, row_kernel_max_heads(d.head_dim));
-  const int hpw_tile = largest_pow2_divisor_upto(rep, 8);
+  const int hpw_tile = largest_pow2_divisor_upto(rep, prefill_waves(d.head_dim));
   const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, hpw_tile);
   if (!row_kernel_supports(d.head_dim, hpw_row))
     return fail(ctx, NVA_E_UNSUPPORTED, "head_dim %d has no row kernel in this build",
@@ -561,9 +562,10 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   PlanKey key;
   key.window = d.sliding_window > 0 ? d.sliding_window : 0;
   key.mfma = mfma ? 1 : 0;
-  key.tile_q = mfma ? prefill_tile_queries(hpw_tile) : 0;
+  key.tile_q = mfma ? prefill_tile_queries(d.head_dim, hpw_tile) : 0;
   key.wg_per_item = d.num_kv_heads * (rep / hpw_row);
   key.blocks_per_cu = mfma ? prefill_blocks_per_cu(d.head_dim, hpw_tile) : 0;
+  key.tile_groups = mfma ? d.num_kv_heads * (rep / hpw_tile) : 0;
   key.tokens = num_tokens;
   key.paged = view.paged;
   key.block_size = view.paged ? view.block_size : 0;

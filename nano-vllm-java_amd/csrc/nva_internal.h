@@ -167,7 +167,11 @@ int prefill_blocks_per_cu(int head_dim, int heads_per_wg);
 // Most pages one prefill key chunk may span (its block ids are staged in LDS).
 constexpr int kPrefillTablePages = 128;
 
+// Waves per prefill workgroup at this head dim; each wave owns 16 queries of one head.
+int prefill_waves(int head_dim);
 // Query rows per prefill workgroup for a given heads-per-workgroup choice.
-inline int prefill_tile_queries(int heads_per_wg) { return 16 * (8 / heads_per_wg); }
+inline int prefill_tile_queries(int head_dim, int heads_per_wg) {
+  return 16 * (prefill_waves(head_dim) / heads_per_wg);
+}
 
 }  // namespace nva

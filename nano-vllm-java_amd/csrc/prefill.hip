@@ -53,6 +53,33 @@ constexpr int kTablePages = kPrefillTablePages;
 namespace {
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// The pair {x[lane], x[lane ^ 16]} (resp. lane ^ 32) in every lane, by gfx950's row-swap
+// instructions: both outputs of the swap of x with itself hold one of the two values.
+struct Pair {
+  float a, b;
+};
+__device__ __forceinline__ Pair pair_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ Pair pair_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+// Max and sum over the four lanes {i, i+16, i+32, i+48}; every lane gets the same bits.
+__device__ __forceinline__ float max4_lanes(float x) {
+  const Pair p = pair_xor16(x);
+  const Pair q = pair_xor32(fmaxf(p.a, p.b));
+  return fmaxf(q.a, q.b);
+}
+__device__ __forceinline__ float sum4_lanes(float x) {
+  const Pair p = pair_xor16(x);
+  const Pair q = pair_xor32(p.a + p.b);
+  return q.a + q.b;
+}
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 
 // Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the block
@@ -73,10 +100,12 @@ __device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *sta
 
 }  // namespace
 
-template <int D, int HPW>
-__global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
-  constexpr int NW = 8;            // waves per workgroup
-  constexpr int KT = 32;           // keys per tile (two 16-key MFMA blocks)
+// NW waves per workgroup, KT keys per tile.  Four waves per SIMD (at most 128 VGPRs) for
+// d <= 128; d = 256 needs more than 128 registers for its Q and O blocks.
+template <int D, int HPW, int KT, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
+prefill_kernel(TileLaunch a) {
+  constexpr int KB = KT / 16;      // 16-key MFMA blocks per key tile
   constexpr int DQ = D / 4;        // QK contraction steps per lane group g: dims [DQ*g, DQ*g+DQ)
   constexpr int NB = D / 16;       // O^T blocks of 16 dims: block 4*hh+bb holds dims 64*hh+4r+bb
   constexpr int H64 = D / 64;      // 64-dim halves of a V row (one ds_read_b128 each)
@@ -100,7 +129,8 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
   const int rep = a.hq / a.hkv;
   const int groups = rep / HPW;
   const int kvh = blockIdx.y / groups;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform, and known to be: every value derived from it lives in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = kvh * rep + (blockIdx.y - kvh * groups) * HPW + wave % HPW;
   const int qb = wave / HPW;
   const int lane = threadIdx.x & 63;
@@ -187,30 +217,39 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
     const bool full = (kt + KT <= whi_min) && (kt >= wlo_max);
 
     // S^T = K Q^T per 16-key block kb: A[key][k] = K[16kb + i][DQ*g + s] (lane i, g),
-    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at position c ^ i.
-    f32x4 st[2];
-    st[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    st[1] = st[0];
+    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at position c ^ i.  Chunk
+    // j of every block is read at once, so each LDS wait is followed by 4 * KB MFMAs that
+    // alternate between the blocks' accumulators.
+    f32x4 st[KB];
+#pragma unroll
+    for (int blk = 0; blk < KB; blk++) st[blk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const float *kb[DQ / 4];
 #pragma unroll
     for (int j = 0; j < DQ / 4; j++) kb[j] = sk + i * D + 4 * (((DQ / 4) * g + j) ^ i);
 #pragma unroll
-    for (int blk = 0; blk < 2; blk++) {
+    for (int s = 0; s < DQ; s += 4) {
+      float4 kk[KB];
 #pragma unroll
-      for (int s = 0; s < DQ; s += 4) {
-        const float4 kk = ld4(kb[s >> 2] + blk * 16 * D);
-        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qr[s], st[blk], 0, 0, 0);
-        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qr[s + 1], st[blk], 0, 0, 0);
-        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[s + 2], st[blk], 0, 0, 0);
-        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[s + 3], st[blk], 0, 0, 0);
-      }
+      for (int blk = 0; blk < KB; blk++) kk[blk] = ld4(kb[s >> 2] + blk * 16 * D);
+#pragma unroll
+      for (int blk = 0; blk < KB; blk++)
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[blk].x, qr[s], st[blk], 0, 0, 0);
+#pragma unroll
+      for (int blk = 0; blk < KB; blk++)
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[blk].y, qr[s + 1], st[blk], 0, 0, 0);
+#pragma unroll
+      for (int blk = 0; blk < KB; blk++)
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[blk].z, qr[s + 2], st[blk], 0, 0, 0);
+#pragma unroll
+      for (int blk = 0; blk < KB; blk++)
+        st[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[blk].w, qr[s + 3], st[blk], 0, 0, 0);
     }
 
     // p[4*blk + v] holds key kt + 16*blk + 4*g + v for query i (log2-scaled).
-    float p[8];
+    float p[4 * KB];
     float mx = -INFINITY;
 #pragma unroll
-    for (int blk = 0; blk < 2; blk++)
+    for (int blk = 0; blk < KB; blk++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         float x = st[blk][v] * sl2;
@@ -221,8 +260,7 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
         p[4 * blk + v] = x;
         mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max4_lanes(mx);
     const bool need = mx > m_run + kLazyRescale;
     if (__any(need)) {
       const float mn = need ? mx : m_run;
@@ -234,7 +272,7 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
     }
     const float ms = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
+    for (int s = 0; s < 4 * KB; s++) {
       p[s] = __builtin_amdgcn_exp2f(p[s] - ms);
       l_run += p[s];
     }
@@ -243,7 +281,7 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
     // operand of block 4*hh + bb is V[key][64*hh + 4*i + bb], one ds_read_b128 per hh.
     const float *vrow = sv + 4 * g * D + 4 * i;
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
+    for (int s = 0; s < 4 * KB; s++) {
       const float *vp = vrow + (16 * (s >> 2) + (s & 3)) * D;
 #pragma unroll
       for (int hh = 0; hh < H64; hh++) {
@@ -273,8 +311,7 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
     compute_tile(kt + KT, sk1, sv1);
   }
 
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  const float l_tot = sum4_lanes(l_run);
   if (!qvalid || !wave_active) continue;
   // Lane (i, g) holds O^T rows r = 4g + v of every block: dims 64*hh + 4r + bb.
   float *op;
@@ -306,14 +343,35 @@ __global__ void __launch_bounds__(512) prefill_kernel(TileLaunch a) {
 
 namespace {
 
+// Keys per tile and waves per workgroup for head dim D.
+template <int D>
+constexpr int key_tile() {
+  return 32;
+}
+template <int D>
+constexpr int tile_waves() {
+  return 8;
+}
+
 template <int D>
 hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
-  const dim3 grid(a.num_slots, a.hkv * ((a.hq / a.hkv) / hpw));
+  constexpr int KT = key_tile<D>(), NW = tile_waves<D>();
+  const dim3 grid(a.num_slots, a.hkv * ((a.hq / a.hkv) / hpw)), block(64 * NW);
   switch (hpw) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1>), grid, dim3(512), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2>), grid, dim3(512), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4>), grid, dim3(512), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8>), grid, dim3(512), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, KT, NW>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, KT, NW>), grid, block, 0, s, a); break;
+    case 4:
+      if constexpr (NW >= 4) {
+        hipLaunchKernelGGL((prefill_kernel<D, 4, KT, NW>), grid, block, 0, s, a);
+        break;
+      }
+      return hipErrorInvalidValue;
+    case 8:
+      if constexpr (NW >= 8) {
+        hipLaunchKernelGGL((prefill_kernel<D, 8, KT, NW>), grid, block, 0, s, a);
+        break;
+      }
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -321,9 +379,16 @@ hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
 
 }  // namespace
 
+int prefill_waves(int head_dim) {
+  if (head_dim == 64) return tile_waves<64>();
+  if (head_dim == 256) return tile_waves<256>();
+  return tile_waves<128>();
+}
+
 bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
   return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
-         (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8);
+         (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8) &&
+         heads_per_wg <= prefill_waves(head_dim);
 }
 
 namespace {
@@ -332,9 +397,10 @@ template <int D, int HPW>
 int blocks_per_cu() {
   static int n = -1;
   if (n < 0) {
+    constexpr int NW = tile_waves<D>();
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, prefill_kernel<D, HPW>, 512, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &b, prefill_kernel<D, HPW, key_tile<D>(), NW>, 64 * NW, 0) != hipSuccess ||
         b < 1)
       b = 1;
     n = b;
@@ -344,11 +410,12 @@ int blocks_per_cu() {
 
 template <int D>
 int blocks_per_cu_d(int hpw) {
+  constexpr int NW = tile_waves<D>();
   switch (hpw) {
     case 1: return blocks_per_cu<D, 1>();
     case 2: return blocks_per_cu<D, 2>();
-    case 4: return blocks_per_cu<D, 4>();
-    default: return blocks_per_cu<D, 8>();
+    case 4: return blocks_per_cu<D, NW >= 4 ? 4 : 1>();
+    default: return blocks_per_cu<D, NW >= 8 ? 8 : 1>();
   }
 }
 
