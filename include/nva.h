@@ -77,8 +77,12 @@ typedef struct nva_rms_norm {
  * (engine/Transformer.java:113-143, 257-271). */
 nva_status nva_ctx_create(int device, nva_ctx **out);
 nva_status nva_ctx_destroy(nva_ctx *ctx);
-/* Use an external HIP stream (hipStream_t) for all later work; NULL restores the context's
- * own stream.  The caller keeps the stream alive while it is set. */
+/* Use an external HIP stream (hipStream_t) for all later work; NULL selects the device's
+ * null stream (HIP's stream 0, torch's default stream).  Until this is called a context uses
+ * its own stream, a blocking stream: work on it is ordered with work on the null stream
+ * (hipMemcpy), so outputs may be copied out with hipMemcpy without nva_ctx_sync().  The
+ * caller keeps an external stream alive while it is set; nva_ctx_stream() returns the
+ * current one (save it first to restore it later). */
 nva_status nva_ctx_set_stream(nva_ctx *ctx, void *hip_stream);
 void *nva_ctx_stream(nva_ctx *ctx);
 /* Blocks until all work enqueued on the context's stream has finished. */

@@ -471,6 +471,9 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
       break;
     }
   }
+  // A paged item of `chunk` keys spans at most (chunk - 1) / BS + 2 pages; the row kernel
+  // stages at most kRowTablePages of them.
+  if (key.paged) chunk = std::min(chunk, (kRowTablePages - 1) * key.block_size);
 
   std::vector<RowItem> items;
   items.reserve(rows.size() + total / chunk + 1);
@@ -822,7 +825,11 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
     ctx->num_cus = prop.multiProcessorCount;
-  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
+  // The context's own stream is a blocking stream, so it is ordered with work on the null
+  // stream (hipMemcpy of inputs and outputs).  The side stream that runs decode rows beside
+  // prefill tiles must overlap with whichever stream is current, so it is non-blocking and
+  // joined through events.
+  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamDefault) != hipSuccess ||
       hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess) {
@@ -868,7 +875,7 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
 
 nva_status nva_ctx_set_stream(nva_ctx *ctx, void *hip_stream) {
   if (!ctx) return NVA_E_ARG;
-  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+  ctx->stream = static_cast<hipStream_t>(hip_stream);  // NULL: the device's null stream
   return NVA_OK;
 }
 

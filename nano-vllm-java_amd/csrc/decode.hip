@@ -62,18 +62,18 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ int64_t kv_row(const KvView &kv, const int32_t *table, int kbase,
-                                          int t) {
+__device__ __forceinline__ int page_of(const KvView &kv, int t) {
+  return kv.bs_shift >= 0 ? t >> kv.bs_shift : t / kv.block_size;
+}
+
+// Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the item's
+// block ids, which starts at page blk0.
+__device__ __forceinline__ int64_t kv_row(const KvView &kv, const int32_t *stab, int blk0,
+                                          int kbase, int t) {
   if (!kv.paged) return (int64_t)kbase + t;
-  int blk, off;
-  if (kv.bs_shift >= 0) {
-    blk = t >> kv.bs_shift;
-    off = t & (kv.block_size - 1);
-  } else {
-    blk = t / kv.block_size;
-    off = t - blk * kv.block_size;
-  }
-  return (int64_t)table[blk] * kv.block_size + off;
+  const int blk = page_of(kv, t);
+  const int off = t - blk * kv.block_size;
+  return (int64_t)stab[blk - blk0] * kv.block_size + off;
 }
 
 }  // namespace
@@ -83,12 +83,13 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   constexpr int LPT = D / 4 < 64 ? D / 4 : 64;  // lanes per K/V row
   constexpr int VPL = D / (4 * LPT);            // float4 per lane per row
   constexpr int TPW = 64 / LPT;                 // rows per wave load instruction
-  constexpr int U = 8 / VPL;                    // rows per stream per group
-  constexpr int G = TPW * U;                    // rows per wave per group
+  constexpr int UH = 4 / VPL > 0 ? 4 / VPL : 1;  // rows per stream per register group
+  constexpr int G = TPW * UH;                    // rows per wave per register group
   constexpr int NS = 4 * TPW;                   // softmax streams per workgroup
   __shared__ float sm_m[NS][HPW];
   __shared__ float sm_l[NS][HPW];
   __shared__ float4 sm_acc[NS][HPW][LPT * VPL];
+  __shared__ int32_t stab[kRowTablePages];  // block ids of the pages this item touches
 
   const RowItem it = a.items[blockIdx.x];
   const int rep = a.hq / a.hkv;
@@ -112,7 +113,16 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   const size_t rs = (size_t)a.hkv * D;
   const float *kp = a.kv.k + (size_t)kvh * D + c * 4;
   const float *vp = a.kv.v + (size_t)kvh * D + c * 4;
-  const int32_t *table = a.kv.paged ? a.kv.table + (size_t)it.seq * a.kv.bt_stride : nullptr;
+  // Stage the item's block ids in LDS once (the host caps items at kRowTablePages pages), so
+  // a row address waits on an LDS read instead of on every K/V load issued before it.
+  int blk0 = 0;
+  if (a.kv.paged) {
+    const int32_t *table = a.kv.table + (size_t)it.seq * a.kv.bt_stride;
+    blk0 = page_of(a.kv, it.kbeg);
+    const int npages = it.kend > it.kbeg ? page_of(a.kv, it.kend - 1) - blk0 + 1 : 0;
+    for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[blk0 + j];
+    __syncthreads();
+  }
 
   float m[HPW], l[HPW];
   float4 acc[HPW][VPL];
@@ -124,25 +134,31 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     for (int j = 0; j < VPL; j++) acc[h][j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
-  for (int g0 = it.kbeg + wave * G; g0 < it.kend; g0 += 4 * G) {
-    float4 kr[U][VPL], vr[U][VPL];
-    bool ok[U];
+  // Two register groups of UH rows per stream: the loads of the next group are issued before
+  // the current one is folded, so every wave keeps loads in flight while it computes.  The
+  // issue is unconditional (keys past the end load the item's first row and are masked), which
+  // keeps the wait before each fold to exactly the current group's loads.
+  float4 kra[UH][VPL], vra[UH][VPL], krb[UH][VPL], vrb[UH][VPL];
+  bool oka[UH], okb[UH];
+  auto issue = [&](int g0, float4(&kr)[UH][VPL], float4(&vr)[UH][VPL], bool(&ok)[UH]) {
 #pragma unroll
-    for (int u = 0; u < U; u++) {
+    for (int u = 0; u < UH; u++) {
       const int t = g0 + u * TPW + sub;
       ok[u] = t < it.kend;
-      const int64_t row = kv_row(a.kv, table, it.kbase, ok[u] ? t : it.kbeg);
+      const int64_t row = kv_row(a.kv, stab, blk0, it.kbase, ok[u] ? t : it.kbeg);
 #pragma unroll
       for (int j = 0; j < VPL; j++) {
         kr[u][j] = ld4_stream(kp + row * rs + LPT * 4 * j);
         vr[u][j] = ld4_stream(vp + row * rs + LPT * 4 * j);
       }
     }
+  };
+  auto fold = [&](const float4(&kr)[UH][VPL], const float4(&vr)[UH][VPL], const bool(&ok)[UH]) {
 #pragma unroll
     for (int h = 0; h < HPW; h++) {
-      float s[U];
+      float s[UH];
 #pragma unroll
-      for (int u = 0; u < U; u++) {
+      for (int u = 0; u < UH; u++) {
         float p = qv[h][0].x * kr[u][0].x;
         p = fmaf(qv[h][0].y, kr[u][0].y, p);
         p = fmaf(qv[h][0].z, kr[u][0].z, p);
@@ -158,7 +174,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       }
       float mx = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < U; u++) {
+      for (int u = 0; u < UH; u++) {
         s[u] = ok[u] ? s[u] * sl2 : -INFINITY;
         mx = fmaxf(mx, s[u]);
       }
@@ -170,7 +186,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
 #pragma unroll
       for (int j = 0; j < VPL; j++) av[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int u = 0; u < U; u++) {
+      for (int u = 0; u < UH; u++) {
         const float w = __builtin_amdgcn_exp2f(s[u] - ms);
         ls += w;
 #pragma unroll
@@ -190,6 +206,21 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
         acc[h][j].w = fmaf(acc[h][j].w, alpha, av[j].w);
       }
       m[h] = mn;
+    }
+  };
+
+  int g0 = it.kbeg + wave * G;
+  if (g0 < it.kend) {
+    issue(g0, kra, vra, oka);
+    for (;;) {
+      issue(g0 + 4 * G, krb, vrb, okb);
+      fold(kra, vra, oka);
+      g0 += 4 * G;
+      if (g0 >= it.kend) break;
+      issue(g0 + 4 * G, kra, vra, oka);
+      fold(krb, vrb, okb);
+      g0 += 4 * G;
+      if (g0 >= it.kend) break;
     }
   }
 

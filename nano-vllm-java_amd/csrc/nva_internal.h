@@ -166,6 +166,8 @@ int prefill_blocks_per_cu(int head_dim, int heads_per_wg);
 
 // Most pages one prefill key chunk may span (its block ids are staged in LDS).
 constexpr int kPrefillTablePages = 128;
+// Most pages one row-kernel work item may span (its block ids are staged in LDS).
+constexpr int kRowTablePages = 64;
 
 // Waves per prefill workgroup at this head dim; each wave owns 16 queries of one head.
 int prefill_waves(int head_dim);
