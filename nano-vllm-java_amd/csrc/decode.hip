@@ -91,11 +91,14 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   __shared__ float4 sm_acc[NS][HPW][LPT * VPL];
   __shared__ int32_t stab[kRowTablePages];  // block ids of the pages this item touches
 
-  const RowItem it = a.items[blockIdx.x];
   const int rep = a.hq / a.hkv;
   const int groups = rep / HPW;
-  const int kvh = blockIdx.y / groups;
-  const int h0 = kvh * rep + (blockIdx.y - kvh * groups) * HPW;
+  const int per_item = a.hkv * groups;
+  const int item = blockIdx.x / per_item;
+  const int gy = blockIdx.x - item * per_item;
+  const RowItem it = a.items[item];
+  const int kvh = gy / groups;
+  const int h0 = kvh * rep + (gy - kvh * groups) * HPW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int sub = lane / LPT;
@@ -384,7 +387,7 @@ namespace {
 
 template <int D>
 hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
-  const dim3 grid(a.num_items, a.hkv * ((a.hq / a.hkv) / hpw));
+  const dim3 grid(a.num_items * (a.hkv * ((a.hq / a.hkv) / hpw)));
   switch (hpw) {
     case 1: hipLaunchKernelGGL((row_attention_kernel<D, 1>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((row_attention_kernel<D, 2>), grid, dim3(256), 0, s, a); break;
