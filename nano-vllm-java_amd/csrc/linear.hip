@@ -37,7 +37,11 @@ __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast
 
 }  // namespace
 
-__global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
+// Two workgroups per CU: at most 128 VGPRs + AGPRs per lane (64 accumulators).
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+linear_kernel(LinearLaunch a) {
+  // Two buffers of the A (x) and B (W) tiles, as separate arrays so the compiler sees that the
+  // copies into one never alias the reads of the other.
   __shared__ __attribute__((aligned(16))) float sa0[BM * BK];
   __shared__ __attribute__((aligned(16))) float sb0[BN * BK];
   __shared__ __attribute__((aligned(16))) float sa1[BM * BK];
@@ -47,7 +51,7 @@ __global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
   const int m0 = blockIdx.y * BM;
   const int kb = blockIdx.z * a.k_per_split;
   const int ke = min(a.k, kb + a.k_per_split);
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
   const int lane = threadIdx.x & 63;
   const int wm = wave >> 1, wn = wave & 1;
   const int i = lane & 31;  // MFMA row (A) / column (B) index of this lane
@@ -83,11 +87,12 @@ __global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
     }
   };
 
-  auto compute = [&](int kt, const float *sa, const float *sb) {
+  // full: every chunk of the tile lies inside the slice (all but a ragged last tile); the
+  // chunks of a ragged tile past the slice end are zeroed.
+  auto compute = [&](int kt, const float *sa, const float *sb, bool full) {
 #pragma unroll
     for (int kk = 0; kk < BK / 8; kk++) {
       const int c = 2 * kk + h;  // this lane's 16-byte chunk of the row
-      const bool valid = kt + 4 * c < ke;
       float4 av[2], bv[2];
 #pragma unroll
       for (int b = 0; b < 2; b++) {
@@ -95,7 +100,10 @@ __global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
         const int rb = wn * 64 + b * 32 + i;
         av[b] = ld4(sa + ra * BK + 4 * (c ^ (ra & 7)));
         bv[b] = ld4(sb + rb * BK + 4 * (c ^ (rb & 7)));
-        if (!valid) {
+      }
+      if (!full && !(kt + 4 * c < ke)) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
           av[b] = make_float4(0.f, 0.f, 0.f, 0.f);
           bv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -112,19 +120,24 @@ __global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
     }
   };
 
+  // Double-buffered K loop with one barrier per tile: at the barrier of tile t every wave has
+  // finished tile t-1, whose buffer is then refilled with tile t+1.
   const int ntiles = (ke - kb + BK - 1) / BK;
   if (ntiles > 0) issue(kb, sa0, sb0);
   for (int t = 0; t < ntiles; t += 2) {
     const int kt = kb + t * BK;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile t landed
     __syncthreads();
     if (t + 1 < ntiles) issue(kt + BK, sa1, sb1);
-    compute(kt, sa0, sb0);
-    if (t + 1 >= ntiles) break;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 2 < ntiles) issue(kt + 2 * BK, sa0, sb0);
-    compute(kt + BK, sa1, sb1);
+    compute(kt, sa0, sb0, kt + BK <= ke);
+    // A conditional block rather than a mid-loop exit, so the accumulators leave the loop
+    // from one place and keep one set of registers.
+    if (t + 1 < ntiles) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (t + 2 < ntiles) issue(kt + 2 * BK, sa0, sb0);
+      compute(kt + BK, sa1, sb1, kt + 2 * BK <= ke);
+    }
   }
 
   const bool direct = a.splits == 1;
