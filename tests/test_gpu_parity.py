@@ -10,19 +10,13 @@ import pytest
 import torch
 
 from cases import Case, rel_l2, small_cases
+from gpu_checks import MAX_ABS, REL_L2, bits, check_attention, dev, load_arena, say
 from nanollvm_amd import Attention, Context, KvCacheArena, RotaryEmbedding
 from nanollvm_amd import workloads as W
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-MAX_ABS = 1e-4
-REL_L2 = 1e-5
-
-
-def say(msg):
-    print(f"[gpu] {msg}", flush=True)
-    sys.stdout.flush()
 
 
 @pytest.fixture(scope="module")
@@ -30,63 +24,6 @@ def ctx():
     c = Context(0)
     yield c
     c.close()
-
-
-def dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
-
-
-def bits(a):
-    return np.ascontiguousarray(a, np.float32).view(np.uint32)
-
-
-def load_arena(ctx, case):
-    wl = case.wl
-    if case.paged:
-        arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
-        arena.write(0, 0, case.k_cache)
-        arena.write(0, 1, case.v_cache)
-    else:
-        arena = KvCacheArena(ctx, 1, 2, 16, wl.hkv, wl.d)
-    return arena
-
-
-def check_attention(ctx, case, name, fused_rope=None):
-    wl = case.wl
-    say(f"{name}: tokens={wl.tokens} hq={wl.hq} hkv={wl.hkv} d={wl.d} W={wl.window}")
-    arena = load_arena(ctx, case)
-    try:
-        ctx.set(**wl.meta.context_args())
-        ctx.bind_kv_cache(arena)
-        attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
-        if fused_rope is None:
-            out = attn.forward(dev(case.q), dev(case.k), dev(case.v), ctx)
-            want, kc, vc = case.oracle(threads=8)
-        else:
-            rope, table = fused_rope
-            q_out = torch.empty(case.q.shape, dtype=torch.float32, device="cuda")
-            k_out = torch.empty(case.k.shape, dtype=torch.float32, device="cuda")
-            out = attn.forward_with_rope(rope, wl.meta.positions, dev(case.q), dev(case.k),
-                                         dev(case.v), ctx, q_out=q_out, k_out=k_out)
-            qr, kr = O.rope_forward(table, wl.meta.positions, case.q, case.k)
-            torch.cuda.synchronize()
-            assert np.array_equal(bits(q_out.cpu().numpy()), bits(qr)), "rotated q not bit-exact"
-            assert np.array_equal(bits(k_out.cpu().numpy()), bits(kr)), "rotated k not bit-exact"
-            case.q, case.k = qr, kr
-            want, kc, vc = case.oracle(threads=8)
-        ctx.sync()
-        got = out.cpu().numpy()
-        err = float(np.max(np.abs(got - want))) if got.size else 0.0
-        rl2 = rel_l2(got, want)
-        say(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e}")
-        assert np.all(np.isfinite(got)), "non-finite output"
-        assert err <= MAX_ABS and rl2 <= REL_L2, (err, rl2)
-        if case.paged:
-            assert np.array_equal(bits(arena.get_key_cache(0)), bits(kc)), "K pages differ"
-            assert np.array_equal(bits(arena.get_value_cache(0)), bits(vc)), "V pages differ"
-    finally:
-        ctx.clear()
-        arena.close()
 
 
 SMALL = small_cases()
