@@ -497,6 +497,18 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     merges.push_back({r.qrow, parts, n, 0});
     parts += n;
   }
+  // The kernels stage an item's (segment's) block ids in LDS; a plan that exceeded those
+  // tables would be a planner bug, reported rather than launched.
+  if (key.paged) {
+    const int bs = key.block_size;
+    for (const RowItem &it : items)
+      if (it.kend > it.kbeg && (it.kend - 1) / bs - it.kbeg / bs + 1 > kRowTablePages)
+        return fail(ctx, NVA_E_UNSUPPORTED, "row item spans more than %d pages", kRowTablePages);
+    for (const TileItem &t : tiles)
+      if (t.ke > t.ks && (t.ke - 1) / bs - t.ks / bs + 1 > kPrefillTablePages)
+        return fail(ctx, NVA_E_UNSUPPORTED, "prefill segment spans more than %d pages",
+                    kPrefillTablePages);
+  }
 
   plan->key = key;
   plan->num_rows = (int)items.size();

@@ -52,3 +52,20 @@ def test_mfma_prefill_matrix(ctx, d, rep, window, layout):
         ctx.set_timing(False)
     say(f"{wl.name}: prefill kernel launches={launches}")
     assert launches >= 1, "the MFMA prefill kernel did not run"
+
+
+@pytest.mark.parametrize("block_size", [1, 16, 256])
+@pytest.mark.parametrize("is_prefill", [False, True])
+def test_long_rows_small_pages(ctx, block_size, is_prefill):
+    """Rows of thousands of keys over pages of 1 and 16 tokens: a work item of the row kernel
+    (or a segment of the prefill kernel) then spans many pages, up to the number whose block ids
+    the kernel stages in LDS; the host caps items and segments at that."""
+    rng = np.random.default_rng(block_size * 7 + int(is_prefill))
+    if is_prefill:
+        seqs = [(2900, 40), (0, 300), (1500, 3)]
+    else:
+        seqs = [(2999, 1), (1499, 1), (4999, 1), (64, 1)]
+    wl = W.build(f"long rows bs{block_size} {'prefill' if is_prefill else 'decode'}", seqs,
+                 is_prefill=is_prefill, hq=4, hkv=2, d=128, scale=float(np.float32(128 ** -0.5)),
+                 rng=rng, block_size=block_size, pool_cap=20000)
+    check_attention(ctx, Case(wl, seed=block_size + 3), wl.name)
