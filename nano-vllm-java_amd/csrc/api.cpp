@@ -1370,15 +1370,29 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
     return fail(ctx, NVA_E_UNSUPPORTED, "linear needs in %% 4 == 0 (got %d)", in);
   if (!aligned16(x) || !aligned16(weight))
     return fail(ctx, NVA_E_ARG, "x and weight must be 16-byte aligned device pointers");
-  // Split K only when the tile grid alone leaves the chip short of two workgroups per CU (the
-  // resident limit at 64 KB of LDS each); every slice keeps at least 4 K tiles.
+  // K slices: the count s that minimises a per-CU cost model.  A CU runs the K tiles of its
+  // workgroups at about the same rate whether one or two are resident, so the kernel takes
+  // ceil(tiles * s / CUs) workgroup rounds of ceil(K tiles / s) K tiles each (about 2.1 us per
+  // 128 x 128 x 32 K tile); s > 1 adds the partial planes (written, then read by the reduce, at
+  // about 5 TB/s) and the reduce launch.  Every slice keeps at least 4 K tiles.
   const int64_t tiles = (int64_t)((out + linear_tile_cols() - 1) / linear_tile_cols()) *
                         ((rows + linear_tile_rows() - 1) / linear_tile_rows());
   const int bk = linear_k_tile();
   const int nkt = (in + bk - 1) / bk;
-  const int64_t want = 2LL * ctx->num_cus;
-  int splits = (int)std::min<int64_t>(std::max<int64_t>(1, (want + tiles - 1) / tiles),
-                                      std::max(1, nkt / 4));
+  const int cus = std::max(1, ctx->num_cus);
+  int splits = 1;
+  double best = 0.0;
+  for (int sl = 1; sl <= std::max(1, nkt / 4); sl++) {
+    const int per = (nkt + sl - 1) / sl;
+    if (sl > 1 && (nkt + per - 1) / per != sl) continue;  // same slices as a smaller count
+    const double rounds = (double)((tiles * sl + cus - 1) / cus);
+    double us = rounds * per * 2.1;
+    if (sl > 1) us += 2.0 * sl * (double)rows * out * 4.0 / 5.0e6 + 3.0;
+    if (sl == 1 || us < best) {
+      best = us;
+      splits = sl;
+    }
+  }
   const int kt_per = (nkt + splits - 1) / splits;
   splits = (nkt + kt_per - 1) / kt_per;
   LinearLaunch a{};
