@@ -1370,6 +1370,23 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
     return fail(ctx, NVA_E_UNSUPPORTED, "linear needs in %% 4 == 0 (got %d)", in);
   if (!aligned16(x) || !aligned16(weight))
     return fail(ctx, NVA_E_ARG, "x and weight must be 16-byte aligned device pointers");
+  if (rows <= linear_gemv_max_rows()) {
+    // A few rows: stream W once (GEMV), no tiles, no K slices.
+    LinearLaunch g{};
+    g.x = x;
+    g.w = weight;
+    g.bias = bias;
+    g.y = y;
+    g.m = rows;
+    g.n = out;
+    g.k = in;
+    g.splits = 1;
+    g.k_per_split = in;
+    Timed tm(ctx, "linear");
+    HIP_TRY(ctx, launch_gemv(g, ctx->stream), "gemv kernel launch");
+    tm.done();
+    return NVA_OK;
+  }
   // K slices: the count s that minimises a per-CU cost model.  A CU runs the K tiles of its
   // workgroups at about the same rate whether one or two are resident, so the kernel takes
   // ceil(tiles * s / CUs) workgroup rounds of ceil(K tiles / s) K tiles each (about 2.1 us per

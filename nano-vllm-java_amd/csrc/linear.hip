@@ -192,6 +192,108 @@ __global__ void __launch_bounds__(256) linear_reduce_kernel(LinearLaunch a) {
   }
 }
 
+// Few rows (decode batches): y = x W^T + bias as a weight-streaming GEMV.  Wave w of
+// workgroup b owns output columns n0 = (4b + w) * CPW .. n0 + CPW - 1 for all M rows: lane l
+// reads the 16-byte chunks l, l + 64, ... of those W rows (non-temporal loads: W is read once)
+// and the same chunks of the M x rows (cached: every wave reads them), keeps M * CPW partial
+// dot products, and folds them across the wave in a fixed DPP order.  HBM bytes: W once, plus
+// x and y; the MFMA tiles would compute 128-row blocks for a handful of rows.
+namespace {
+
+typedef float gv4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld4_stream(const float *p) {
+  const gv4 t = __builtin_nontemporal_load(reinterpret_cast<const gv4 *>(p));
+  return make_float4(t.x, t.y, t.z, t.w);
+}
+
+// Sum over the 64 lanes; lane 63 holds the total.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x114, 0xF, 0xE, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x118, 0xF, 0xC, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0.0f, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
+}  // namespace
+
+template <int M, int CPW>
+__global__ void __launch_bounds__(256) gemv_kernel(LinearLaunch a) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + wave) * CPW;
+  if (n0 >= a.n) return;  // uniform per wave
+  const int chunks = a.k >> 2;
+  float acc[M][CPW];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < CPW; j++) acc[m][j] = 0.0f;
+  const float *wr[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; j++) wr[j] = a.w + (size_t)min(n0 + j, a.n - 1) * a.k;
+  const int rows = min(M, a.m);
+  // U chunks per lane in flight, W and x loads issued together before any arithmetic; chunks
+  // past the end (and x rows past M) load chunk 0 / row 0 and are skipped.
+  constexpr int U = M <= 2 ? 4 : 2;
+  for (int c0 = lane; c0 < chunks; c0 += U * 64) {
+    float4 wv[U][CPW], xv[U][M];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      ok[u] = c0 + 64 * u < chunks;
+      const int c = ok[u] ? c0 + 64 * u : 0;
+#pragma unroll
+      for (int j = 0; j < CPW; j++) wv[u][j] = ld4_stream(wr[j] + 4 * c);
+#pragma unroll
+      for (int m = 0; m < M; m++)
+        xv[u][m] = *reinterpret_cast<const float4 *>(a.x + (size_t)(m < rows ? m : 0) * a.k + 4 * c);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (!ok[u]) break;
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        if (m < rows) {
+#pragma unroll
+          for (int j = 0; j < CPW; j++) {
+            acc[m][j] = fmaf(xv[u][m].x, wv[u][j].x, acc[m][j]);
+            acc[m][j] = fmaf(xv[u][m].y, wv[u][j].y, acc[m][j]);
+            acc[m][j] = fmaf(xv[u][m].z, wv[u][j].z, acc[m][j]);
+            acc[m][j] = fmaf(xv[u][m].w, wv[u][j].w, acc[m][j]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+    if (m >= rows) break;
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+      const float t = wave_sum(acc[m][j]);
+      const int n = n0 + j;
+      if (lane == 63 && n < a.n) a.y[(size_t)m * a.n + n] = a.bias ? t + a.bias[n] : t;
+    }
+  }
+}
+
+int linear_gemv_max_rows() { return 8; }
+
+hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s) {
+  constexpr int CPW = 2;
+  const dim3 grid((a.n + 4 * CPW - 1) / (4 * CPW));
+  if (a.m <= 1) hipLaunchKernelGGL((gemv_kernel<1, CPW>), grid, dim3(256), 0, s, a);
+  else if (a.m <= 2) hipLaunchKernelGGL((gemv_kernel<2, CPW>), grid, dim3(256), 0, s, a);
+  else if (a.m <= 4) hipLaunchKernelGGL((gemv_kernel<4, CPW>), grid, dim3(256), 0, s, a);
+  else if (a.m <= 8) hipLaunchKernelGGL((gemv_kernel<8, CPW>), grid, dim3(256), 0, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t launch_linear(const LinearLaunch &a, hipStream_t s) {
   if (a.m <= 0 || a.n <= 0) return hipSuccess;
   const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM, a.splits);

@@ -60,6 +60,10 @@ def check(got, want, name):
 @pytest.mark.parametrize("rows,inf,outf,bias", [
     (1, 2048, 1024, False),    # one decode row, Qwen3-0.6B o_proj
     (8, 2048, 1024, True),     # 8-row decode batch
+    (2, 4096, 2560, True),     # GEMV path, Qwen3-4B o_proj
+    (3, 260, 200, False),      # GEMV path, rows short of its 4-row form, ragged N and K
+    (5, 1028, 7, True),        # GEMV path, 8-row form, fewer columns than one workgroup
+    (9, 260, 200, True),       # first row count past the GEMV path
     (37, 260, 200, True),      # ragged M, N, K (K % 32 != 0)
     (130, 2048, 1024, False),  # M tail past one 128-row tile
     (256, 2048, 1024, True),   # 256-row decode batch
