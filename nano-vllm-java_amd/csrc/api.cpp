@@ -497,6 +497,12 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     merges.push_back({r.qrow, parts, n, 0});
     parts += n;
   }
+  // Longest items first: the workgroups dispatched last are the short row tails, so the chip
+  // drains quickly at the end of the launch.  Items carry their own partial slot, so the
+  // order does not change any result.
+  std::stable_sort(items.begin(), items.end(), [](const RowItem &x, const RowItem &y) {
+    return x.kend - x.kbeg > y.kend - y.kbeg;
+  });
   // The kernels stage an item's (segment's) block ids in LDS; a plan that exceeded those
   // tables would be a planner bug, reported rather than launched.
   if (key.paged) {
