@@ -356,11 +356,13 @@ def _extra_builders():
         "c5-qwen3-4b-mixed": W.qwen3_4b_mixed,
         "gemma3-prefill-local": lambda: W.gemma3_prefill(local=True),
         "gemma3-prefill-global": lambda: W.gemma3_prefill(local=False),
+        "gemma4-prefill-global": W.gemma4_prefill_global,
     }
 
 
 EXTRA = ["c1-qwen3-decode-b8", "c3-gemma3-decode-local", "c3-gemma3-decode-global",
-         "c5-qwen3-4b-mixed", "gemma3-prefill-local", "gemma3-prefill-global"]
+         "c5-qwen3-4b-mixed", "gemma3-prefill-local", "gemma3-prefill-global",
+         "gemma4-prefill-global"]
 
 
 def bench_extra(args, ctx):

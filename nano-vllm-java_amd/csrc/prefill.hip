@@ -101,7 +101,8 @@ __device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *sta
 }  // namespace
 
 // NW waves per workgroup, KT keys per tile.  Four waves per SIMD (at most 128 VGPRs) for
-// d <= 128; d = 256 needs more than 128 registers for its Q and O blocks.
+// d <= 128; d = 256 needs more than 128 registers for its Q and O blocks, and d = 512 keeps
+// its O blocks in AGPRs (one wave per SIMD).
 template <int D, int HPW, int KT, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
 prefill_kernel(TileLaunch a) {
@@ -110,10 +111,10 @@ prefill_kernel(TileLaunch a) {
   constexpr int NB = D / 16;       // O^T blocks of 16 dims: block 4*hh+bb holds dims 64*hh+4r+bb
   constexpr int H64 = D / 64;      // 64-dim halves of a V row (one ds_read_b128 each)
   constexpr int C4 = D / 4;        // 16-byte chunks per K/V row
-  constexpr int RPI = 64 / C4;     // rows per wave load instruction
-  constexpr int LPW = KT / RPI / NW;  // load instructions per wave per tensor per tile
+  constexpr int NI = KT * C4 / 64;  // load instructions per tensor per tile (64 chunks each)
+  constexpr int LPW = NI / NW;     // load instructions per wave per tensor per tile
   constexpr int TILE = KT * D;     // floats per K (or V) tile
-  static_assert(LPW >= 1, "tile too small for the workgroup");
+  static_assert(LPW >= 1 && NI % NW == 0, "tile does not split evenly over the waves");
   __shared__ __attribute__((aligned(16))) float sk0[TILE];
   __shared__ __attribute__((aligned(16))) float sv0[TILE];
   __shared__ __attribute__((aligned(16))) float sk1[TILE];
@@ -189,26 +190,36 @@ prefill_kernel(TileLaunch a) {
     for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[j];
     __syncthreads();
   }
-  const int lrow = lane / C4;
-  const int lpos = lane - lrow * C4;
-
+  // Load instruction gi copies chunks [64 gi, 64 gi + 64) of the tile in row-major order (a
+  // whole number of rows for d <= 256, half a row at d = 512): lane l takes chunk q = 64 gi + l,
+  // i.e. position q % C4 of tile row q / C4.
+  const int lrow = C4 <= 64 ? lane / C4 : 0;  // rows within one instruction (d <= 256)
+  const int lpos = C4 <= 64 ? lane - lrow * C4 : 0;
   auto issue_tile = [&](int kt, float *dk, float *dv) {
 #pragma unroll
     for (int p = 0; p < LPW; p++) {
-      const int gi = p * NW + wave;  // instruction index: rows [gi*RPI, gi*RPI + RPI)
-      const int r = gi * RPI + lrow;
+      const int gi = p * NW + wave;
+      int r, pos;
+      if constexpr (C4 <= 64) {
+        r = gi * (64 / C4) + lrow;
+        pos = lpos;
+      } else {
+        const int q = gi * 64 + lane;
+        r = q / C4;
+        pos = q - r * C4;
+      }
       const int key = min(kt + r, it.ke - 1);  // rows past the chunk are loaded but masked
       const int64_t row = tile_row(a.kv, stab, blk0, it.kbase, key);
       // K chunks are XOR-swizzled by (row & 15) for the column reads of QK; V rows are read
       // along the row, which is conflict-free unswizzled.
-      const float *gk = kbase + row * rs + (lpos ^ (r & 15)) * 4;
-      const float *gv = vbase + row * rs + lpos * 4;
+      const float *gk = kbase + row * rs + (pos ^ (r & 15)) * 4;
+      const float *gv = vbase + row * rs + pos * 4;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void *)gk,
-          (__attribute__((address_space(3))) void *)(dk + gi * RPI * D), 16, 0, 0);
+          (__attribute__((address_space(3))) void *)(dk + gi * 256), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void *)gv,
-          (__attribute__((address_space(3))) void *)(dv + gi * RPI * D), 16, 0, 0);
+          (__attribute__((address_space(3))) void *)(dv + gi * 256), 16, 0, 0);
     }
   };
 
@@ -346,11 +357,11 @@ namespace {
 // Keys per tile and waves per workgroup for head dim D.
 template <int D>
 constexpr int key_tile() {
-  return 32;
+  return D == 512 ? 16 : 32;
 }
 template <int D>
 constexpr int tile_waves() {
-  return 8;
+  return D == 512 ? 4 : 8;
 }
 
 template <int D>
@@ -382,11 +393,12 @@ hipError_t launch_prefill_d(const TileLaunch &a, int hpw, hipStream_t s) {
 int prefill_waves(int head_dim) {
   if (head_dim == 64) return tile_waves<64>();
   if (head_dim == 256) return tile_waves<256>();
+  if (head_dim == 512) return tile_waves<512>();
   return tile_waves<128>();
 }
 
 bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
-  return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+  return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) &&
          (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8) &&
          heads_per_wg <= prefill_waves(head_dim);
 }
@@ -424,6 +436,7 @@ int blocks_per_cu_d(int hpw) {
 int prefill_blocks_per_cu(int head_dim, int heads_per_wg) {
   if (head_dim == 64) return blocks_per_cu_d<64>(heads_per_wg);
   if (head_dim == 256) return blocks_per_cu_d<256>(heads_per_wg);
+  if (head_dim == 512) return blocks_per_cu_d<512>(heads_per_wg);
   return blocks_per_cu_d<128>(heads_per_wg);
 }
 
@@ -433,6 +446,7 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int hpw, hipStream_t s) {
     case 64: return launch_prefill_d<64>(a, hpw, s);
     case 128: return launch_prefill_d<128>(a, hpw, s);
     case 256: return launch_prefill_d<256>(a, hpw, s);
+    case 512: return launch_prefill_d<512>(a, hpw, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -177,6 +177,16 @@ def gemma3_prefill(seed=0, local=True) -> Workload:
                  rope_theta=1e4 if local else 1e6, max_pos=32768)
 
 
+def gemma4_prefill_global(seed=0) -> Workload:
+    """Gemma-4-text-shaped global (full-attention) layer, varlen prefill 512/1024/1536/2048:
+    8 q heads / 1 kv head, head dim 512 (global_head_dim), scale 1.0 (Config.attentionScale:
+    q/k are RMS-normed), no window (ModelSupportTest.java:101-118 text_config)."""
+    rng = np.random.default_rng(seed)
+    return build("gemma4-text global layer varlen prefill 512/1024/1536/2048 (8q/1kv, d=512)",
+                 [(0, 512), (0, 1024), (0, 1536), (0, 2048)], is_prefill=True, hq=8, hkv=1,
+                 d=512, scale=1.0, window=0, rng=rng, rope_theta=1e6, max_pos=32768)
+
+
 def qwen3_decode_large(seed=0, batch=256, lo=128, hi=32768) -> Workload:
     rng = np.random.default_rng(seed)
     ctx = loguniform_lengths(rng, batch, lo, hi)

@@ -1,6 +1,6 @@
 """Parity of the fp32 MFMA prefill kernel over its whole configuration space, against the oracle.
 
-The prefill kernel is instantiated for head dims 64, 128 and 256 and for 1, 2, 4 or 8 query
+The prefill kernel is instantiated for head dims 64, 128, 256 and 512 and for 1, 2, 4 or 8 query
 heads per workgroup (GQA ratio 1, 2, 4, 8).  Each case mixes ragged sequences: a prefix hit
 (full pages), a mid-page chunk start, a two-query sequence (the smallest MFMA tile), a one-query
 row (the row kernel) and lengths that leave partial query tiles and partial key tiles.  It runs
@@ -32,7 +32,7 @@ def ctx():
 @pytest.mark.parametrize("layout", ["paged16", "paged256", "dense"])
 @pytest.mark.parametrize("window", [0, 37])
 @pytest.mark.parametrize("rep", [1, 2, 4, 8])
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [64, 128, 256, 512])
 def test_mfma_prefill_matrix(ctx, d, rep, window, layout):
     hkv = 2
     hq = hkv * rep
