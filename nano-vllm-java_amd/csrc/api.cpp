@@ -406,7 +406,9 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     constexpr int KT = 32;
     int64_t total = 0;
     for (const TileItem &t : tiles) total += (t.ke - t.ks + KT - 1) / KT;
-    const int64_t resident = (int64_t)ctx->num_cus * key.blocks_per_cu;
+    // A mixed plan runs its rows on a second stream beside the tiles; one tile workgroup per
+    // CU leaves registers for row workgroups on every CU.
+    const int64_t resident = (int64_t)ctx->num_cus * (rows.empty() ? key.blocks_per_cu : 1);
     slots = (int)std::max<int64_t>(1, std::min<int64_t>(total, resident / key.tile_groups));
     const int64_t page_cap =
         paged ? (int64_t)(kPrefillTablePages - 2) * key.block_size / KT * KT : INT32_MAX;
