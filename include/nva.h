@@ -270,6 +270,20 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
                                            const float *k, const float *v, int num_tokens,
                                            float *q_out, float *k_out, float *out);
 
+/* The same, reading q, k and v from the packed qkv_proj output qkv [num_tokens,
+ * (num_heads + 2 * num_kv_heads) * head_dim] -- per token the q heads, then the k heads, then
+ * the v heads -- which the model layers split with Ops.splitLast before normHeads and RoPE
+ * (models/internal/Qwen3ForCausalLM.java:210-214, Gemma3ForCausalLM.java:144-148,
+ * LlamaForCausalLM.java:144-148).  The kernels read the packed rows in place, so no split copy is made.  Results are
+ * identical to nva_norm_rope_attention_forward on the split tensors. */
+nva_status nva_qkv_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                               const nva_rms_norm *q_norm,
+                                               const nva_rms_norm *k_norm,
+                                               const nva_rms_norm *v_norm,
+                                               const nva_attn_desc *desc, const float *qkv,
+                                               int num_tokens, float *q_out, float *k_out,
+                                               float *out);
+
 #ifdef __cplusplus
 }
 #endif

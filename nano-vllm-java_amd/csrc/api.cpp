@@ -1289,13 +1289,14 @@ nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *
                                          num_tokens, q_out, k_out, out);
 }
 
-nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
-                                           const nva_rms_norm *q_norm,
-                                           const nva_rms_norm *k_norm,
-                                           const nva_rms_norm *v_norm,
-                                           const nva_attn_desc *desc, const float *q,
-                                           const float *k, const float *v, int num_tokens,
-                                           float *q_out, float *k_out, float *out) {
+// The head norms, RoPE, the store and attention with q, k, v rows read at token strides q_ld,
+// k_ld, v_ld (floats): [T, heads, d] inputs, or the packed qkv_proj output.
+static nva_status norm_rope_attention(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                      const nva_rms_norm *q_norm, const nva_rms_norm *k_norm,
+                                      const nva_rms_norm *v_norm, const nva_attn_desc *desc,
+                                      const float *q, const float *k, const float *v, int q_ld,
+                                      int k_ld, int v_ld, int num_tokens, float *q_out,
+                                      float *k_out, float *out) {
   if (!ctx) return NVA_E_ARG;
   nva_status st = check_forward(ctx, kv, desc, num_tokens);
   if (st != NVA_OK) return st;
@@ -1325,9 +1326,11 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
     HIP_TRY(ctx, ctx->d_k_rot.reserve(kn * 4 + 16), "rotated k scratch");
     k_out = static_cast<float *>(ctx->d_k_rot.ptr);
   }
-  // Dense prefill attends over the step's own k/v rows, so a normalised v must exist as rows.
+  // Dense prefill attends over the step's own k/v rows, so a normalised v (or the v of packed
+  // inputs) must exist as contiguous rows.
+  const bool v_packed = v_ld != d.num_kv_heads * d.head_dim;
   float *v_out = nullptr;
-  if (v_norm && dense) {
+  if ((v_norm || v_packed) && dense) {
     HIP_TRY(ctx, ctx->d_v_norm.reserve(kn * 4 + 16), "normalised v scratch");
     v_out = static_cast<float *>(ctx->d_v_norm.ptr);
   }
@@ -1341,6 +1344,9 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
   a.q = q;
   a.k = k;
   a.v = v;
+  a.q_ld = q_ld;
+  a.k_ld = k_ld;
+  a.v_ld = v_ld;
   a.q_out = q_out;
   a.k_out = k_out;
   a.v_out = v_out;
@@ -1365,6 +1371,41 @@ nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_r
     tm.done();
   }
   return attention_after_store(ctx, kv, d, q_out, k_out, v_out ? v_out : v, num_tokens, out);
+}
+
+nva_status nva_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                           const nva_rms_norm *q_norm,
+                                           const nva_rms_norm *k_norm,
+                                           const nva_rms_norm *v_norm,
+                                           const nva_attn_desc *desc, const float *q,
+                                           const float *k, const float *v, int num_tokens,
+                                           float *q_out, float *k_out, float *out) {
+  if (!ctx) return NVA_E_ARG;
+  if (!desc) return fail(ctx, NVA_E_ARG, "attention descriptor is null");
+  return norm_rope_attention(ctx, kv, rope, q_norm, k_norm, v_norm, desc, q, k, v,
+                             desc->num_heads * desc->head_dim,
+                             desc->num_kv_heads * desc->head_dim,
+                             desc->num_kv_heads * desc->head_dim, num_tokens, q_out, k_out, out);
+}
+
+nva_status nva_qkv_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,
+                                               const nva_rms_norm *q_norm,
+                                               const nva_rms_norm *k_norm,
+                                               const nva_rms_norm *v_norm,
+                                               const nva_attn_desc *desc, const float *qkv,
+                                               int num_tokens, float *q_out, float *k_out,
+                                               float *out) {
+  if (!ctx) return NVA_E_ARG;
+  if (!desc) return fail(ctx, NVA_E_ARG, "attention descriptor is null");
+  if (!qkv) return fail(ctx, NVA_E_ARG, "qkv is required");
+  const int64_t qs = (int64_t)desc->num_heads * desc->head_dim;
+  const int64_t ks = (int64_t)desc->num_kv_heads * desc->head_dim;
+  if (qs <= 0 || ks <= 0 || qs + 2 * ks > INT32_MAX)
+    return fail(ctx, NVA_E_ARG, "bad head counts %d/%d x %d", desc->num_heads,
+                desc->num_kv_heads, desc->head_dim);
+  const int ld = (int)(qs + 2 * ks);
+  return norm_rope_attention(ctx, kv, rope, q_norm, k_norm, v_norm, desc, qkv, qkv + qs,
+                             qkv + qs + ks, ld, ld, ld, num_tokens, q_out, k_out, out);
 }
 
 nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,

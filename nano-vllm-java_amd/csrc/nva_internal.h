@@ -115,6 +115,7 @@ struct RopeStoreLaunch {
   int32_t tokens, hq, hk, head_dim;
   HeadNorm qn, kn, vn;        // per-head RMSNorm applied to q, k, v before rotation / store
   int32_t iters_per_wg;       // row kernel: row iterations per workgroup (set by the launcher)
+  int32_t q_ld, k_ld, v_ld;   // floats per token of the q, k, v inputs (0: hq*d, hk*d, hk*d)
 };
 
 // Standalone RMSNorm over rows of any width (RMSNorm.forward).

@@ -97,9 +97,9 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
   const int ngroups = d >> 2;
   float *inv_lds = norm_lds + (size_t)nrows * ngroups;
   auto row_ptr = [&](int r) -> const float * {
-    if (r < a.hq) return a.q + ((size_t)t * a.hq + r) * d;
-    if (r < a.hq + a.hk) return a.k + ((size_t)t * a.hk + (r - a.hq)) * d;
-    return a.v + ((size_t)t * a.hk + (r - a.hq - a.hk)) * d;
+    if (r < a.hq) return a.q + (size_t)t * a.q_ld + (size_t)r * d;
+    if (r < a.hq + a.hk) return a.k + (size_t)t * a.k_ld + (size_t)(r - a.hq) * d;
+    return a.v + (size_t)t * a.v_ld + (size_t)(r - a.hq - a.hk) * d;
   };
   auto row_norm = [&](int r) -> const HeadNorm & {
     return r < a.hq ? a.qn : (r < a.hq + a.hk ? a.kn : a.vn);
@@ -138,8 +138,8 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
       const int i = (it - hh * per_head) * step;
       const bool isq = hh < a.hq;
       const int h = isq ? hh : hh - a.hq;
-      const size_t base = ((size_t)t * (isq ? a.hq : a.hk) + h) * d;
-      const float *in = (isq ? a.q : a.k) + base;
+      const size_t base = ((size_t)t * (isq ? a.hq : a.hk) + h) * d;  // output row
+      const float *in = (isq ? a.q + (size_t)t * a.q_ld : a.k + (size_t)t * a.k_ld) + (size_t)h * d;
       const HeadNorm &nm = isq ? a.qn : a.kn;
       const float inv = nm.enabled ? inv_lds[hh] : 1.0f;
       if (vec) {
@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
     }
   } else if (store) {
     // Store without rotation (Attention.forward's own store of already-rotated k).
-    const float *kin = a.k + (size_t)t * krow;
+    const float *kin = a.k + (size_t)t * a.k_ld;
     if ((krow & 3) == 0) {
       for (int i = threadIdx.x * 4; i < (int)krow; i += blockDim.x * 4) st4(kc + i, ld4(kin + i));
     } else {
@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
   if (a.vn.enabled && (store || a.v_out)) {
     // Normalised v rows (Gemma 4's weightless v norm) to the pages and/or v_out; a float4 never
     // straddles two heads.
-    const float *vin = a.v + (size_t)t * krow;
+    const float *vin = a.v + (size_t)t * a.v_ld;
     float *vo = a.v_out ? a.v_out + (size_t)t * krow : nullptr;
     const int step = (d & 3) == 0 ? 4 : 1;
     for (int i = threadIdx.x * step; i < (int)krow; i += blockDim.x * step) {
@@ -223,12 +223,21 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
         if (vo) vo[i] = y;
       }
     }
-  } else if (store) {
-    const float *vin = a.v + (size_t)t * krow;
+  } else if (store || a.v_out) {
+    // v rows to the pages and/or as contiguous rows (v_out: packed inputs, dense prefill).
+    const float *vin = a.v + (size_t)t * a.v_ld;
+    float *vo = a.v_out ? a.v_out + (size_t)t * krow : nullptr;
     if ((krow & 3) == 0) {
-      for (int i = threadIdx.x * 4; i < (int)krow; i += blockDim.x * 4) st4(vc + i, ld4(vin + i));
+      for (int i = threadIdx.x * 4; i < (int)krow; i += blockDim.x * 4) {
+        const float4 y = ld4(vin + i);
+        if (store) st4(vc + i, y);
+        if (vo) st4(vo + i, y);
+      }
     } else {
-      for (int i = threadIdx.x; i < (int)krow; i += blockDim.x) vc[i] = vin[i];
+      for (int i = threadIdx.x; i < (int)krow; i += blockDim.x) {
+        if (store) vc[i] = vin[i];
+        if (vo) vo[i] = vin[i];
+      }
     }
   }
 }
@@ -284,9 +293,9 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
       const int rc = live[i] ? r : 0;
       kind[i] = rc < rq ? 0 : (rc < rq + rk ? 1 : 2);  // q, k, v
       h[i] = kind[i] == 0 ? rc : (kind[i] == 1 ? rc - rq : rc - rq - rk);
-      const int heads = kind[i] == 0 ? a.hq : a.hk;
-      const float *src = (kind[i] == 0 ? a.q : (kind[i] == 1 ? a.k : a.v)) +
-                         ((size_t)t * heads + h[i]) * D;
+      const int ld = kind[i] == 0 ? a.q_ld : (kind[i] == 1 ? a.k_ld : a.v_ld);
+      const float *src = (kind[i] == 0 ? a.q : (kind[i] == 1 ? a.k : a.v)) + (size_t)t * ld +
+                         (size_t)h[i] * D;
 #pragma unroll
       for (int j = 0; j < VPL; j++)
         x[i][j] = live[i] ? ld4(src + 4 * (c + LPR * j)) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -452,8 +461,12 @@ hipError_t launch_rows(const RopeStoreLaunch &a, hipStream_t s, int num_cus) {
 
 }  // namespace
 
-hipError_t launch_rope_store(const RopeStoreLaunch &a, hipStream_t s, int num_cus) {
-  if (a.tokens <= 0) return hipSuccess;
+hipError_t launch_rope_store(const RopeStoreLaunch &in, hipStream_t s, int num_cus) {
+  if (in.tokens <= 0) return hipSuccess;
+  RopeStoreLaunch a = in;  // inputs with no stride given are contiguous [T, heads, d]
+  if (!a.q_ld) a.q_ld = a.hq * a.head_dim;
+  if (!a.k_ld) a.k_ld = a.hk * a.head_dim;
+  if (!a.v_ld) a.v_ld = a.hk * a.head_dim;
   // Row kernel for the head dims it is instantiated for; the per-token kernel otherwise.
   switch (a.head_dim) {
     case 8: return launch_rows<2, 1>(a, s, num_cus);

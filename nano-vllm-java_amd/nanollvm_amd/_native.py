@@ -134,6 +134,9 @@ SIGNATURES = {
     "nva_norm_rope_attention_forward": ([_vp, _vp, _vp, _pnorm, _pnorm, _pnorm,
                                          ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci, _vp, _vp,
                                          _vp], _st),
+    "nva_qkv_norm_rope_attention_forward": ([_vp, _vp, _vp, _pnorm, _pnorm, _pnorm,
+                                             ctypes.POINTER(AttnDesc), _vp, _ci, _vp, _vp, _vp],
+                                            _st),
 }
 
 _lib = None

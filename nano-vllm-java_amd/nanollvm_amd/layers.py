@@ -517,3 +517,37 @@ class Attention:
             _dev(k, "k"), _dev(v, "v"), q.shape[0], _dev(q_out, "q_out"), _dev(k_out, "k_out"),
             _dev(out, "out")), "Attention.forward (q/k norm + RoPE)")
         return out
+
+    def forward_packed_qkv(self, rope: RotaryEmbedding, positions, qkv: torch.Tensor,
+                           ctx: Context, q_norm: Optional[RMSNorm] = None,
+                           k_norm: Optional[RMSNorm] = None, v_norm: Optional[RMSNorm] = None,
+                           q_out: Optional[torch.Tensor] = None,
+                           k_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """forward_with_norm_rope on the packed qkv_proj output [T, (Hq + 2 Hkv) * d] (q heads,
+        k heads, v heads per token), read in place instead of split by Ops.splitLast
+        (Qwen3ForCausalLM.java:210-214)."""
+        width = (self.num_heads + 2 * self.num_kv_heads) * self.head_dim
+        if qkv.dim() != 2 or qkv.shape[1] != width:
+            raise IllegalArgumentException(f"qkv must be [T, {width}]")
+        if qkv.dtype != torch.float32 or not qkv.is_contiguous():
+            raise IllegalArgumentException("qkv must be a contiguous float32 tensor")
+        T = qkv.shape[0]
+        for t, shape in ((q_out, (T, self.num_heads, self.head_dim)),
+                         (k_out, (T, self.num_kv_heads, self.head_dim))):
+            if t is not None and tuple(t.shape) != shape:
+                raise IllegalArgumentException("q_out/k_out must be [T, heads, headDim]")
+        for n in (q_norm, k_norm, v_norm):
+            if n is not None and n.weight is not None and n.weight.numel() != self.head_dim:
+                raise IllegalArgumentException("head norm weights must have headDim entries")
+        if positions is not None:
+            ctx.set_positions(positions)
+        arena = ctx.kv_cache()
+        out = torch.empty((T, self.num_heads, self.head_dim), dtype=torch.float32,
+                          device=qkv.device)
+        _check(ctx.handle, N.load().nva_qkv_norm_rope_attention_forward(
+            ctx.handle, arena.handle if arena is not None else None, rope.handle,
+            None if q_norm is None else q_norm.desc(), None if k_norm is None else k_norm.desc(),
+            None if v_norm is None else v_norm.desc(), ctypes.byref(self._desc),
+            _dev(qkv, "qkv"), T, _dev(q_out, "q_out"), _dev(k_out, "k_out"), _dev(out, "out")),
+            "Attention.forward (packed qkv)")
+        return out
