@@ -16,6 +16,8 @@
  *     q/out [tokens, num_heads, head_dim], k/v [tokens, num_kv_heads, head_dim].
  *     Step metadata (cu_seqlens, slots, tables, positions) are HOST pointers; they are copied
  *     to the device once per nva_step_set() and shared by every layer of that step.
+ *   - A forward call with num_tokens == 0 (or rows == 0) does nothing and succeeds; its tensor
+ *     pointers may then be NULL (the reference returns an empty tensor).
  *   - All work is enqueued on the context's HIP stream and is asynchronous unless stated.
  *   - A context is used by one host thread at a time (the reference's single generate thread,
  *     Attention.java:41-44); there is no internal locking.

@@ -599,8 +599,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
 
   if (!plan->covers_all) {
     // Rows outside every sequence stay zero, as Tensor.zeros in the reference.
-    HIP_TRY(ctx, hipMemsetAsync(out, 0, (size_t)num_tokens * d.num_heads * d.head_dim * 4,
-                                ctx->stream),
+    HIP_TRY(ctx, launch_zero(out, (size_t)num_tokens * d.num_heads * d.head_dim, ctx->stream),
             "zero output");
   }
   char *pbase = static_cast<char *>(plan->dev.ptr);
@@ -1219,6 +1218,7 @@ nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, 
   if (!rope) return fail(ctx, NVA_E_ARG, "RoPE table is null");
   if (!ctx->has_step) return fail(ctx, NVA_E_NO_STEP, "no step metadata set on the context");
   if (num_tokens < 0 || hq < 0 || hk < 0) return fail(ctx, NVA_E_ARG, "negative shape");
+  if (num_tokens == 0) return NVA_OK;  // empty batch: empty outputs, no pointers needed
   if (!q || !k || !q_out || !k_out) return fail(ctx, NVA_E_ARG, "q, k, q_out, k_out required");
   if (!aligned16(q) || !aligned16(k) || !aligned16(q_out) || !aligned16(k_out))
     return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
@@ -1251,6 +1251,7 @@ nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *
   if (!ctx) return NVA_E_ARG;
   nva_status st = check_forward(ctx, kv, desc, num_tokens);
   if (st != NVA_OK) return st;
+  if (num_tokens == 0) return NVA_OK;  // empty batch: an empty output, as Tensor.zeros(0, ...)
   if (!q || !out) return fail(ctx, NVA_E_ARG, "q and out are required");
   if (!aligned16(q) || !aligned16(out) || (k && !aligned16(k)) || (v && !aligned16(v)))
     return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
@@ -1304,6 +1305,7 @@ static nva_status norm_rope_attention(nva_ctx *ctx, nva_kv *kv, const nva_rope *
   if (rope->head_size != desc->head_dim)
     return fail(ctx, NVA_E_ARG, "RoPE head size %d != headDim %d", rope->head_size,
                 desc->head_dim);
+  if (num_tokens == 0) return NVA_OK;  // empty batch
   if (!q || !k || !v || !out) return fail(ctx, NVA_E_ARG, "q, k, v and out are required");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
       (q_out && !aligned16(q_out)) || (k_out && !aligned16(k_out)))
@@ -1397,13 +1399,16 @@ nva_status nva_qkv_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const n
                                                float *out) {
   if (!ctx) return NVA_E_ARG;
   if (!desc) return fail(ctx, NVA_E_ARG, "attention descriptor is null");
-  if (!qkv) return fail(ctx, NVA_E_ARG, "qkv is required");
+  if (!qkv && num_tokens != 0) return fail(ctx, NVA_E_ARG, "qkv is required");
   const int64_t qs = (int64_t)desc->num_heads * desc->head_dim;
   const int64_t ks = (int64_t)desc->num_kv_heads * desc->head_dim;
   if (qs <= 0 || ks <= 0 || qs + 2 * ks > INT32_MAX)
     return fail(ctx, NVA_E_ARG, "bad head counts %d/%d x %d", desc->num_heads,
                 desc->num_kv_heads, desc->head_dim);
   const int ld = (int)(qs + 2 * ks);
+  if (!qkv)  // empty batch: checks only
+    return norm_rope_attention(ctx, kv, rope, q_norm, k_norm, v_norm, desc, nullptr, nullptr,
+                               nullptr, ld, ld, ld, 0, q_out, k_out, out);
   return norm_rope_attention(ctx, kv, rope, q_norm, k_norm, v_norm, desc, qkv, qkv + qs,
                              qkv + qs + ks, ld, ld, ld, num_tokens, q_out, k_out, out);
 }

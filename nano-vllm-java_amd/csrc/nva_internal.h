@@ -149,6 +149,7 @@ hipError_t launch_rms_norm(const NormLaunch &a, hipStream_t s);
 size_t rope_store_norm_lds(const RopeStoreLaunch &a);
 constexpr size_t kRopeNormMaxLds = 64 * 1024;
 hipError_t launch_gather(const GatherLaunch &a, hipStream_t s);
+hipError_t launch_zero(float *out, size_t n, hipStream_t s);
 hipError_t launch_linear(const LinearLaunch &a, hipStream_t s);
 // Weight-streaming GEMV for at most linear_gemv_max_rows() rows (no split, no partials).
 hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s);

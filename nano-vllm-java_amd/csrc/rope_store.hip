@@ -418,6 +418,13 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(NormLaunch a) {
   for (int i = threadIdx.x; i < a.width; i += blockDim.x) o[i] = norm1(x[i], inv, a.norm, i);
 }
 
+// out[0 .. n) = 0 (rows no sequence covers stay zero, as Tensor.zeros in the reference).  A
+// kernel rather than hipMemsetAsync so that a caller may capture the call in a graph.
+__global__ void __launch_bounds__(256) zero_kernel(float *out, size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = 0.0f;
+}
+
 // gatherKvCache (layers/Attention.java:201-216): rows of the producer layer's pages at the
 // step's slots into dense [T, Hkv, d]; negative slots give zero rows.
 __global__ void __launch_bounds__(256) gather_kernel(GatherLaunch a) {
@@ -487,6 +494,13 @@ hipError_t launch_rope_store(const RopeStoreLaunch &in, hipStream_t s, int num_c
 hipError_t launch_rms_norm(const NormLaunch &a, hipStream_t s) {
   if (a.rows <= 0 || a.width <= 0) return hipSuccess;
   hipLaunchKernelGGL(rms_norm_kernel, dim3(a.rows), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero(float *out, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, s, out, n);
   return hipGetLastError();
 }
 
