@@ -92,7 +92,9 @@ nva_status nva_ctx_sync(nva_ctx *ctx);
 const char *nva_last_error(nva_ctx *ctx);
 const char *nva_status_string(nva_status status);
 /* Per-kernel timing with HIP events on the context's stream (off by default).  Kernel names:
- * "rope_store", "store", "decode", "merge", "prefill", "gather". */
+ * "rope_store", "store", "decode", "merge", "prefill", "gather", "linear", "rms_norm";
+ * "attention" spans the attention kernels of one call (decode and prefill kernels that
+ * overlap count once). */
 nva_status nva_ctx_set_timing(nva_ctx *ctx, int enable);
 nva_status nva_ctx_kernel_stats(nva_ctx *ctx, const char *kernel, int64_t *launches,
                                 double *total_ms);

@@ -108,8 +108,10 @@ struct PlanKey {
   int tokens;                  // rows of q / out in the forward call
   int paged;                   // keys through block tables (else dense k/v rows)
   int block_size, num_blocks;  // arena geometry the tables are checked against
+  int head_dim, num_heads, num_kv_heads;  // size the work of a mixed plan's two kernels
   bool operator==(const PlanKey &o) const {
     return window == o.window && mfma == o.mfma && tile_q == o.tile_q &&
+           head_dim == o.head_dim && num_heads == o.num_heads && num_kv_heads == o.num_kv_heads &&
            wg_per_item == o.wg_per_item && blocks_per_cu == o.blocks_per_cu &&
            tile_groups == o.tile_groups && tokens == o.tokens && paged == o.paged &&
            block_size == o.block_size && num_blocks == o.num_blocks;
@@ -286,6 +288,29 @@ int largest_pow2_divisor_upto(int rep, int cap) {
   return h;
 }
 
+// CUs for the tile grid of a mixed plan, one tile workgroup on each; the rows run on the other
+// CUs and in the room left on the tile CUs.  The tile share f of the CUs minimises the longer of
+// the two kernels: the tiles' time scales as 1/f, while the rows, being HBM-bound, keep
+// 1 - f^1.8 of the whole chip's bandwidth on the remaining CUs (the split-KV decode on
+// CU-masked streams holds 72% of it on half of the CUs, 60% on 3/8, 42% on 1/4).  Solo rates:
+// rows 6.5 TB/s, tiles 100 / 80 / 70 TFLOP/s at head dim <= 128 / 256 / 512.
+int64_t mixed_tile_cus(int num_cus, double row_bytes, double tile_flops, int head_dim) {
+  const double tr = row_bytes / 6.5e12;
+  const double tt =
+      tile_flops / (head_dim <= 128 ? 100e12 : head_dim <= 256 ? 80e12 : 70e12);
+  int best_s = 8;
+  double best = 1e300;
+  for (int s = 1; s < 16; s++) {
+    const double f = s / 16.0;
+    const double t = std::max(tr / (1.0 - std::pow(f, 1.8)), tt / f);
+    if (t < best) {
+      best = t;
+      best_s = s;
+    }
+  }
+  return (int64_t)num_cus * best_s / 16;
+}
+
 // One query row of the row kernel before splitting.
 struct Row {
   int qrow, seq, kbase, kbeg, kend;
@@ -406,9 +431,24 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     constexpr int KT = 32;
     int64_t total = 0;
     for (const TileItem &t : tiles) total += (t.ke - t.ks + KT - 1) / KT;
-    // A mixed plan runs its rows on a second stream beside the tiles; one tile workgroup per
-    // CU leaves registers for row workgroups on every CU.
-    const int64_t resident = (int64_t)ctx->num_cus * (rows.empty() ? key.blocks_per_cu : 1);
+    // A mixed plan runs its rows on a second stream beside the tiles; the tile grid then has
+    // one workgroup on each of a share of the CUs, and the rows take the rest.
+    int64_t resident = (int64_t)ctx->num_cus * key.blocks_per_cu;
+    if (!rows.empty()) {
+      double row_bytes = 0.0, pairs = 0.0;
+      for (const Row &r : rows) row_bytes += std::max(0, r.kend - r.kbeg);
+      row_bytes *= 8.0 * key.num_kv_heads * key.head_dim;
+      for (const TileItem &t : tiles) {
+        const int n = std::min(key.tile_q, t.qlen - t.q0);
+        for (int i = 0; i < n; i++) {
+          const int aq = t.klen - t.qlen + t.q0 + i;
+          pairs += W > 0 ? std::min(aq + 1, W) : aq + 1;
+        }
+      }
+      const double flops = 4.0 * key.head_dim * key.num_heads * pairs;
+      resident = std::max<int64_t>(key.tile_groups,
+                                   mixed_tile_cus(ctx->num_cus, row_bytes, flops, key.head_dim));
+    }
     slots = (int)std::max<int64_t>(1, std::min<int64_t>(total, resident / key.tile_groups));
     const int64_t page_cap =
         paged ? (int64_t)(kPrefillTablePages - 2) * key.block_size / KT * KT : INT32_MAX;
@@ -593,10 +633,15 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   key.paged = view.paged;
   key.block_size = view.paged ? view.block_size : 0;
   key.num_blocks = view.paged ? num_blocks : 0;
+  key.head_dim = d.head_dim;
+  key.num_heads = d.num_heads;
+  key.num_kv_heads = d.num_kv_heads;
   Plan *plan = nullptr;
   nva_status st = get_plan(ctx, key, &plan);
   if (st != NVA_OK) return st;
 
+  // "attention" times the whole part below, kernels that overlap counted once.
+  Timed span(ctx, "attention");
   if (!plan->covers_all) {
     // Rows outside every sequence stay zero, as Tensor.zeros in the reference.
     HIP_TRY(ctx, launch_zero(out, (size_t)num_tokens * d.num_heads * d.head_dim, ctx->stream),
@@ -611,33 +656,11 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   float *pm = static_cast<float *>(ctx->d_part.ptr);
   // A mixed step (MFMA tiles and rows in one plan) runs the HBM-bound rows on the side stream
   // while the MFMA-bound tiles run on the main stream; both write disjoint partials, and the
-  // main stream waits for the side stream before the merge.
+  // main stream waits for the side stream before the merge.  The tiles are issued first: the
+  // plan sized their grid to a share of the CUs, which it only gets if the rows do not fill
+  // the chip before it.
   const bool fork = plan->num_tiles > 0 && plan->num_rows > 0;
-  hipStream_t row_stream = ctx->stream;
-  if (fork) {
-    HIP_TRY(ctx, hipEventRecord(ctx->fork_ev, ctx->stream), "fork record");
-    HIP_TRY(ctx, hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0), "fork wait");
-    row_stream = ctx->side_stream;
-  }
-  if (plan->num_rows > 0) {
-    RowLaunch r;
-    r.q = q;
-    r.out = out;
-    r.kv = view;
-    r.items = reinterpret_cast<const RowItem *>(pbase + plan->off_rows);
-    r.num_items = plan->num_rows;
-    r.hq = d.num_heads;
-    r.hkv = d.num_kv_heads;
-    r.head_dim = d.head_dim;
-    r.scale = d.scale;
-    r.part_m = pm;
-    r.part_l = pm + parts;
-    r.part_acc = pm + 2 * parts;
-    Timed tm(ctx, "decode", row_stream);
-    HIP_TRY(ctx, launch_row_attention(r, hpw_row, row_stream), "decode kernel launch");
-    tm.done();
-  }
-  if (fork) HIP_TRY(ctx, hipEventRecord(ctx->join_ev, ctx->side_stream), "join record");
+  if (fork) HIP_TRY(ctx, hipEventRecord(ctx->fork_ev, ctx->stream), "fork record");
   if (plan->num_tiles > 0) {
     TileLaunch t;
     t.q = q;
@@ -659,7 +682,33 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     HIP_TRY(ctx, launch_prefill_tiles(t, hpw_tile, ctx->stream), "prefill kernel launch");
     tm.done();
   }
-  if (fork) HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0), "join wait");
+  if (plan->num_rows > 0) {
+    hipStream_t row_stream = ctx->stream;
+    if (fork) {
+      HIP_TRY(ctx, hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0), "fork wait");
+      row_stream = ctx->side_stream;
+    }
+    RowLaunch r;
+    r.q = q;
+    r.out = out;
+    r.kv = view;
+    r.items = reinterpret_cast<const RowItem *>(pbase + plan->off_rows);
+    r.num_items = plan->num_rows;
+    r.hq = d.num_heads;
+    r.hkv = d.num_kv_heads;
+    r.head_dim = d.head_dim;
+    r.scale = d.scale;
+    r.part_m = pm;
+    r.part_l = pm + parts;
+    r.part_acc = pm + 2 * parts;
+    Timed tm(ctx, "decode", row_stream);
+    HIP_TRY(ctx, launch_row_attention(r, hpw_row, row_stream), "decode kernel launch");
+    tm.done();
+  }
+  if (fork) {
+    HIP_TRY(ctx, hipEventRecord(ctx->join_ev, ctx->side_stream), "join record");
+    HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0), "join wait");
+  }
   if (plan->num_merge > 0) {
     MergeLaunch mg;
     mg.out = out;
@@ -674,6 +723,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     HIP_TRY(ctx, launch_merge(mg, plan->max_parts, ctx->stream), "merge kernel launch");
     tm.done();
   }
+  span.done();
   return NVA_OK;
 }
 
