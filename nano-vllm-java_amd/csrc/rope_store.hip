@@ -249,7 +249,7 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
 // slot are loaded once per lane and reused by every row.  Lane c of a group holds the float4
 // groups c + LPR * j (j < VPL) of the row.  The norm's group sums are folded in index order with
 // DPP shifts; the rotation partner of a first-half element sits LPR / 2 lanes away (VPL = 1) or
-// in the lane's own second float4 (VPL = 2, d = 512).
+// in the lane's own column VPL/2 further on (VPL > 1).
 template <int LPR, int VPL>
 __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
   constexpr int D = 4 * LPR * VPL;
@@ -271,13 +271,25 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
   const size_t krow = (size_t)a.hk * D;
 
   const bool rotate = a.positions != nullptr;
-  float4 cv[VPL], sv[VPL];
+  constexpr int H2 = VPL > 1 ? VPL / 2 : 1;  // cos|sin float4s a lane needs
+  static_assert(VPL == 1 || VPL % 2 == 0, "a split row holds both halves in its own lanes");
+  float4 cv[H2], sv[H2];
   if (rotate) {
     const float *cs = a.cos_sin + (size_t)a.positions[t] * D;
-    // VPL == 1: lane c < LPR/2 rotates x1 = elements 4c.., the others x2 = HALF + 4(c - LPR/2).
-    const int i0 = VPL == 1 ? 4 * (c < LPR / 2 ? c : c - LPR / 2) : 4 * c;
-    cv[0] = ld4(cs + i0);
-    sv[0] = ld4(cs + HALF + i0);
+    if constexpr (VPL == 1) {
+      // Lane c < LPR/2 rotates x1 = elements 4c.., the others x2 = HALF + 4(c - LPR/2).
+      const int i0 = 4 * (c < LPR / 2 ? c : c - LPR / 2);
+      cv[0] = ld4(cs + i0);
+      sv[0] = ld4(cs + HALF + i0);
+    } else {
+      // Columns j < VPL/2 hold first-half elements 4(c + LPR j); column j + VPL/2 holds their
+      // partners HALF elements on.
+#pragma unroll
+      for (int j = 0; j < H2; j++) {
+        cv[j] = ld4(cs + 4 * (c + LPR * j));
+        sv[j] = ld4(cs + HALF + 4 * (c + LPR * j));
+      }
+    }
   }
   const int32_t slot = a.slots ? a.slots[t] : -1;
   const bool store = store_any && slot >= 0;
@@ -306,26 +318,23 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
       if (ib + i >= it1) break;  // uniform over the workgroup (the DPP fold spans the wave)
       const HeadNorm &nm = kind[i] == 0 ? a.qn : (kind[i] == 1 ? a.kn : a.vn);
       if (nm.enabled) {
-        // ScalarFloatKernels.sumSquares order: group sums added in group-index order.
+        // ScalarFloatKernels.sumSquares order: group sums added in group-index order, as a
+        // shift-and-add chain per float4 column j: after step s, lane l holds the in-order sum
+        // of the s group sums ending at lane l, starting from 0 (lane 0 shifts in 0), so after
+        // LPR steps the group's last lane holds ((0 + p0) + p1) + ... + p[LPR-1] -- the same
+        // additions in the same order, with no LDS traffic.  Column j > 0 continues the total
+        // of the columns before it: the group's first lane adds that total to its own group
+        // sum first, which is the chain's first addition (0 + that sum is exact).
         float sum = 0.0f;
-        if constexpr (VPL == 1) {
-          // Serial fold as a shift-and-add chain: after step s, lane j holds the in-order sum
-          // of the s group sums ending at lane j, starting from 0 (lane 0 shifts in 0), so
-          // after LPR steps the group's last lane holds ((0 + p0) + p1) + ... + p[LPR-1] --
-          // the same additions in the same order, with no LDS traffic.
-          const float p = group_sq(x[i][0].x, x[i][0].y, x[i][0].z, x[i][0].w);
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+          float p = group_sq(x[i][j].x, x[i][j].y, x[i][j].z, x[i][j].w);
+          if (j > 0 && c == 0) p = add_rn(sum, p);
           float acc = 0.0f;
 #pragma unroll
           for (int l = 0; l < LPR; l++)
             acc = add_rn(__builtin_amdgcn_update_dpp(0.0f, acc, 0x138, 0xF, 0xF, false), p);
           sum = __shfl(acc, base + LPR - 1);
-        } else {
-#pragma unroll
-          for (int j = 0; j < VPL; j++) {
-            const float p = group_sq(x[i][j].x, x[i][j].y, x[i][j].z, x[i][j].w);
-#pragma unroll
-            for (int l = 0; l < LPR; l++) sum = add_rn(sum, __shfl(p, base + l));
-          }
         }
         const float var = sum / (float)D;  // correctly rounded (HIP default)
         const float inv = (float)(1.0 / sqrt((double)add_rn(var, nm.eps)));
@@ -354,15 +363,19 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
             o[0].w = x[i][0].w * cv[0].w + y.w * sv[0].w;
           }
         } else {
-          // VPL == 2: x[0] = elements [4c, 4c+4) (first half), x[1] = [HALF + 4c, +4).
-          o[0].x = x[i][0].x * cv[0].x - x[i][1].x * sv[0].x;
-          o[0].y = x[i][0].y * cv[0].y - x[i][1].y * sv[0].y;
-          o[0].z = x[i][0].z * cv[0].z - x[i][1].z * sv[0].z;
-          o[0].w = x[i][0].w * cv[0].w - x[i][1].w * sv[0].w;
-          o[1].x = x[i][1].x * cv[0].x + x[i][0].x * sv[0].x;
-          o[1].y = x[i][1].y * cv[0].y + x[i][0].y * sv[0].y;
-          o[1].z = x[i][1].z * cv[0].z + x[i][0].z * sv[0].z;
-          o[1].w = x[i][1].w * cv[0].w + x[i][0].w * sv[0].w;
+          // Column j (first half) and column j + VPL/2 (its partners).
+#pragma unroll
+          for (int j = 0; j < H2; j++) {
+            const float4 u = x[i][j], w = x[i][j + H2];
+            o[j].x = u.x * cv[j].x - w.x * sv[j].x;
+            o[j].y = u.y * cv[j].y - w.y * sv[j].y;
+            o[j].z = u.z * cv[j].z - w.z * sv[j].z;
+            o[j].w = u.w * cv[j].w - w.w * sv[j].w;
+            o[j + H2].x = w.x * cv[j].x + u.x * sv[j].x;
+            o[j + H2].y = w.y * cv[j].y + u.y * sv[j].y;
+            o[j + H2].z = w.z * cv[j].z + u.z * sv[j].z;
+            o[j + H2].w = w.w * cv[j].w + u.w * sv[j].w;
+          }
         }
       } else {
 #pragma unroll

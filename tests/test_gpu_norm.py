@@ -165,3 +165,19 @@ def test_fused_norm_gemma3_decode_full_size(ctx):
     kw = (0.1 * rng.standard_normal(256)).astype(np.float32)
     check_fused(ctx, Case(wl, seed=0), "norm gemma3 local decode", qw, kw, one_plus=True,
                 max_pos=wl.max_pos, theta=wl.rope_theta)
+
+
+@pytest.mark.parametrize("is_prefill", [True, False])
+def test_fused_norm_gemma4_global_d512(ctx, is_prefill):
+    """Gemma-4-text global layer shape (8 q / 1 kv heads, d = 512, scale 1; Gemma4ForCausalLM.
+    java:164-197): q/k norm weights and the weightless v norm.  A 512-wide row holds two float4
+    columns per lane, so its sum of squares folds 128 group sums in two chains; q, k and the
+    pages must equal the oracle bit for bit."""
+    rng = np.random.default_rng(9)
+    seqs = [(0, 70), (33, 41), (5, 1)] if is_prefill else [(c - 1, 1) for c in (3, 64, 200, 517)]
+    wl = W.build("gemma4 global d512", seqs, is_prefill=is_prefill, hq=8, hkv=1, d=512,
+                 scale=1.0, rng=rng, block_size=16)
+    qw = (1.0 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    kw = (1.0 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    check_fused(ctx, Case(wl, seed=3), f"norm gemma4 d512 prefill={is_prefill}", qw, kw,
+                v_norm=True, max_pos=1024, theta=1e6)
