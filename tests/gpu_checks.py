@@ -74,3 +74,34 @@ def check_attention(ctx, case, name, fused_rope=None):
     finally:
         ctx.clear()
         arena.close()
+
+
+def torch_view(ptr, count):
+    """A float32 torch tensor over device memory the library owns (no copy)."""
+
+    class _Cai:
+        pass
+
+    obj = _Cai()
+    obj.__cuda_array_interface__ = {"shape": (count,), "typestr": "<f4", "data": (ptr, False),
+                                    "version": 2, "strides": None}
+    return torch.as_tensor(obj, device="cuda")
+
+
+def arena_views(arena, layer=0):
+    """Device views of one layer's K and V pages, [num_blocks, block_size * Hkv * d] each."""
+    k_ptr, v_ptr, nbytes = arena.device_ptrs(layer)
+    n = nbytes // 4
+    nb = arena.num_blocks
+    return torch_view(k_ptr, n).view(nb, -1), torch_view(v_ptr, n).view(nb, -1)
+
+
+def fill_normal(arena, seed, layer=0):
+    """Seeded N(0, 1) pages, written on the device."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    for t in arena_views(arena, layer):
+        flat = t.view(-1)
+        for s in range(0, flat.numel(), 1 << 28):
+            flat[s:s + (1 << 28)].normal_(generator=g)
+    torch.cuda.synchronize()
