@@ -359,12 +359,14 @@ def _extra_builders():
         "gemma3-prefill-local": lambda: W.gemma3_prefill(local=True),
         "gemma3-prefill-global": lambda: W.gemma3_prefill(local=False),
         "gemma4-prefill-global": W.gemma4_prefill_global,
+        "c4-share-head-1of8": lambda: W.qwen3_decode_large_share(8, "head"),
+        "c4-share-seq-1of8": lambda: W.qwen3_decode_large_share(8, "seq"),
     }
 
 
 EXTRA = ["c1-qwen3-decode-b8", "c3-gemma3-decode-local", "c3-gemma3-decode-global",
          "c5-qwen3-4b-mixed", "gemma3-prefill-local", "gemma3-prefill-global",
-         "gemma4-prefill-global"]
+         "gemma4-prefill-global", "c4-share-head-1of8", "c4-share-seq-1of8"]
 
 
 def bench_extra(args, ctx):

@@ -194,6 +194,22 @@ def qwen3_decode_large(seed=0, batch=256, lo=128, hi=32768) -> Workload:
                  is_prefill=False, hq=16, hkv=8, d=128, scale=QWEN_SCALE, rng=rng)
 
 
+def qwen3_decode_large_share(ways=8, by="head", seed=0, batch=256, lo=128, hi=32768) -> Workload:
+    """One GPU's share of the headline decode sharded ``ways`` ways with no exchange: by KV
+    head (all rows, 16/ways q heads over 8/ways KV heads) or by sequence (every ways-th row,
+    all heads).  Same contexts as qwen3_decode_large."""
+    rng = np.random.default_rng(seed)
+    ctx = loguniform_lengths(rng, batch, lo, hi)
+    if by == "head":
+        return build(f"qwen3-0.6b decode B={batch} ctx log-U[{lo},{hi}], 1/{ways} of the KV heads",
+                     [(c - 1, 1) for c in ctx], is_prefill=False, hq=16 // ways, hkv=8 // ways,
+                     d=128, scale=QWEN_SCALE, rng=rng)
+    rows = ctx[::ways]
+    return build(f"qwen3-0.6b decode ctx log-U[{lo},{hi}], every {ways}th of {batch} rows",
+                 [(c - 1, 1) for c in rows], is_prefill=False, hq=16, hkv=8, d=128,
+                 scale=QWEN_SCALE, rng=rng)
+
+
 def qwen3_4b_mixed(seed=0, chunks=4, chunk=512, prior_hi=4096, rows=64, ctx_lo=4096,
                    ctx_hi=16384) -> Workload:
     rng = np.random.default_rng(seed)
