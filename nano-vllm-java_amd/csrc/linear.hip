@@ -6,8 +6,9 @@
 // output in its gemv panel order; here the sum runs over MFMA steps and split-K slices, so the
 // result agrees to fp32 rounding (checked against the oracle within the attention tolerance).
 //
-// Mapping onto CDNA4.  A workgroup (4 waves, 256 threads) owns a 128 x 128 tile of y and one
-// K slice; wave (wm, wn) computes 64 x 64 of it as 2 x 2 blocks of v_mfma_f32_32x32x2_f32.
+// Mapping onto CDNA4.  A workgroup owns a 128 x 128 tile of y and one K slice: four waves of
+// 64 x 64 (2 x 2 blocks of v_mfma_f32_32x32x2_f32), or, when the grid has no more workgroups
+// than CUs, eight waves of 32 x 64, so each SIMD still has two waves to switch between.
 //   * x and W are both K-contiguous, so the A operand (x rows) and the B operand (W rows) are
 //     read the same way: for each 8-wide K chunk a lane (i, h) reads one float4 of its row
 //     (elements 4h .. 4h + 3), which feeds 4 MFMA steps -- step s contracts k = 4h + s, a
@@ -37,9 +38,15 @@ __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast
 
 }  // namespace
 
-// Two workgroups per CU: at most 128 VGPRs + AGPRs per lane (64 accumulators).
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+// WM x 2 waves; wave (wm, wn) owns 128/WM rows x 64 columns of the tile as MB x 2 blocks of
+// 32 x 32.  WM = 2: four waves of 64 x 64 (64 accumulators), two workgroups per CU; WM = 4:
+// eight waves of 32 x 64 (32 accumulators), two workgroups per CU and four waves per SIMD.
+template <int WM>
+__global__ void __launch_bounds__(64 * WM * 2) __attribute__((amdgpu_waves_per_eu(WM == 4 ? 4 : 2)))
 linear_kernel(LinearLaunch a) {
+  constexpr int NW = WM * 2;       // waves
+  constexpr int MB = BM / WM / 32; // 32-row blocks per wave
+  constexpr int LPW = 16 / NW;     // tile-copy instructions per wave per operand
   // Two buffers of the A (x) and B (W) tiles, as separate arrays so the compiler sees that the
   // copies into one never alias the reads of the other.
   __shared__ __attribute__((aligned(16))) float sa0[BM * BK];
@@ -53,13 +60,13 @@ linear_kernel(LinearLaunch a) {
   const int ke = min(a.k, kb + a.k_per_split);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
   const int lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 1, wn = wave & 1;  // wave = 2 * wm + wn
   const int i = lane & 31;  // MFMA row (A) / column (B) index of this lane
   const int h = lane >> 5;  // which half of an 8-wide K chunk this lane supplies
 
-  f32x16 acc[2][2];
+  f32x16 acc[MB][2];
 #pragma unroll
-  for (int bm = 0; bm < 2; bm++)
+  for (int bm = 0; bm < MB; bm++)
 #pragma unroll
     for (int bn = 0; bn < 2; bn++)
 #pragma unroll
@@ -71,8 +78,8 @@ linear_kernel(LinearLaunch a) {
   const int lpos = lane & 7;
   auto issue = [&](int kt, float *da, float *db) {
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const int g = 4 * p + wave;
+    for (int p = 0; p < LPW; p++) {
+      const int g = NW * p + wave;
       const int r = 8 * g + lrow;
       int kc = kt + 4 * (lpos ^ (r & 7));
       kc = kc < ke ? kc : kb;  // past the slice: a valid address, zeroed at use
@@ -93,23 +100,25 @@ linear_kernel(LinearLaunch a) {
 #pragma unroll
     for (int kk = 0; kk < BK / 8; kk++) {
       const int c = 2 * kk + h;  // this lane's 16-byte chunk of the row
-      float4 av[2], bv[2];
+      float4 av[MB], bv[2];
+#pragma unroll
+      for (int b = 0; b < MB; b++) {
+        const int ra = wm * 32 * MB + b * 32 + i;
+        av[b] = ld4(sa + ra * BK + 4 * (c ^ (ra & 7)));
+      }
 #pragma unroll
       for (int b = 0; b < 2; b++) {
-        const int ra = wm * 64 + b * 32 + i;
         const int rb = wn * 64 + b * 32 + i;
-        av[b] = ld4(sa + ra * BK + 4 * (c ^ (ra & 7)));
         bv[b] = ld4(sb + rb * BK + 4 * (c ^ (rb & 7)));
       }
       if (!full && !(kt + 4 * c < ke)) {
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-          av[b] = make_float4(0.f, 0.f, 0.f, 0.f);
-          bv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int b = 0; b < MB; b++) av[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int b = 0; b < 2; b++) bv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
-      for (int bm = 0; bm < 2; bm++)
+      for (int bm = 0; bm < MB; bm++)
 #pragma unroll
         for (int bn = 0; bn < 2; bn++) {
           acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].x, bv[bn].x, acc[bm][bn], 0, 0, 0);
@@ -143,7 +152,7 @@ linear_kernel(LinearLaunch a) {
   const bool direct = a.splits == 1;
   float *dst = direct ? a.y : a.part + (size_t)blockIdx.z * a.m * a.n;
 #pragma unroll
-  for (int bm = 0; bm < 2; bm++)
+  for (int bm = 0; bm < MB; bm++)
 #pragma unroll
     for (int bn = 0; bn < 2; bn++) {
       const int col = n0 + wn * 64 + bn * 32 + i;
@@ -151,7 +160,7 @@ linear_kernel(LinearLaunch a) {
       const float bias = direct && a.bias ? a.bias[col] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int row = m0 + wm * 32 * MB + bm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (row < a.m) dst[(size_t)row * a.n + col] = acc[bm][bn][r] + bias;
       }
     }
@@ -297,7 +306,10 @@ hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s) {
 hipError_t launch_linear(const LinearLaunch &a, hipStream_t s) {
   if (a.m <= 0 || a.n <= 0) return hipSuccess;
   const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM, a.splits);
-  hipLaunchKernelGGL(linear_kernel, grid, dim3(256), 0, s, a);
+  if (a.waves_m == 4)
+    hipLaunchKernelGGL(linear_kernel<4>, grid, dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL(linear_kernel<2>, grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   const size_t units = (a.n & 3) == 0 ? (size_t)a.m * a.n / 4 : (size_t)a.m * a.n;

@@ -133,6 +133,7 @@ struct LinearLaunch {
   float *part;  // [splits, m, n] partial sums when splits > 1
   int32_t m, n, k;
   int32_t splits, k_per_split;
+  int32_t waves_m;  // waves along the tile's rows: 2 (four 64 x 64 waves) or 4 (eight 32 x 64)
 };
 
 struct GatherLaunch {
