@@ -17,7 +17,7 @@
 //   * Key tiles of 32 rows of K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
 //     register staging), double-buffered so the next tile streams in while this one is used;
 //     one barrier per tile.  Rows are stored unpadded; K rows have their 16-byte chunks
-//     XOR-swizzled by (row & 15) so the column reads of QK are conflict-free, V rows are read
+//     XOR-swizzled by (row & 7) so the column reads of QK are conflict-free, V rows are read
 //     along the row and need no swizzle.  The block ids of the segment's pages are staged in LDS
 //     once, so a paged tile load never waits on a global table read.
 //   * Per tile each wave computes (D = 128)
@@ -210,9 +210,9 @@ prefill_kernel(TileLaunch a) {
       }
       const int key = min(kt + r, it.ke - 1);  // rows past the chunk are loaded but masked
       const int64_t row = tile_row(a.kv, stab, blk0, it.kbase, key);
-      // K chunks are XOR-swizzled by (row & 15) for the column reads of QK; V rows are read
+      // K chunks are XOR-swizzled by (row & 7) for the column reads of QK; V rows are read
       // along the row, which is conflict-free unswizzled.
-      const float *gk = kbase + row * rs + (pos ^ (r & 15)) * 4;
+      const float *gk = kbase + row * rs + (pos ^ (r & 7)) * 4;
       const float *gv = vbase + row * rs + pos * 4;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void *)gk,
@@ -228,7 +228,7 @@ prefill_kernel(TileLaunch a) {
     const bool full = (kt + KT <= whi_min) && (kt >= wlo_max);
 
     // S^T = K Q^T per 16-key block kb: A[key][k] = K[16kb + i][DQ*g + s] (lane i, g),
-    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at position c ^ i.  Chunk
+    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at position c ^ (i & 7).  Chunk
     // j of every block is read at once, so each LDS wait is followed by 4 * KB MFMAs that
     // alternate between the blocks' accumulators.
     f32x4 st[KB];
@@ -236,7 +236,7 @@ prefill_kernel(TileLaunch a) {
     for (int blk = 0; blk < KB; blk++) st[blk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const float *kb[DQ / 4];
 #pragma unroll
-    for (int j = 0; j < DQ / 4; j++) kb[j] = sk + i * D + 4 * (((DQ / 4) * g + j) ^ i);
+    for (int j = 0; j < DQ / 4; j++) kb[j] = sk + i * D + 4 * (((DQ / 4) * g + j) ^ (i & 7));
 #pragma unroll
     for (int s = 0; s < DQ; s += 4) {
       float4 kk[KB];
