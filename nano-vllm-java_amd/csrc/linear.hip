@@ -15,7 +15,8 @@
 //     permutation of the chunk that A and B share.
 //   * K tiles of 32 are copied HBM -> LDS with global_load_lds_dwordx4, double-buffered, one
 //     barrier per tile; each 128-byte row of a tile has its 16-byte chunks XOR-swizzled by
-//     (row & 7), so the 8 lanes of a ds_read_b128 phase hit 8 different bank groups.
+//     ((row >> 1) & 7): measured free of LDS bank conflicts (row & 7: half of the LDS-active
+//     cycles were conflict stalls).
 //   * Output block layout (32 x 32, 16 values per lane): value r of lane (i, h) is row
 //     8 * (r / 4) + 4 * h + r % 4, column i -- lanes 0..31 write 128 contiguous bytes.
 //   * When the tile grid alone cannot fill the chip (decode: a few rows), K is split over
@@ -73,7 +74,7 @@ linear_kernel(LinearLaunch a) {
       for (int r = 0; r < 16; r++) acc[bm][bn][r] = 0.0f;
 
   // Copy instruction p of wave w moves rows [8g, 8g + 8) of a tile, g = 4p + w: lane l takes
-  // row 8g + l / 8, LDS chunk position l % 8, i.e. global chunk (l % 8) ^ (row & 7).
+  // row 8g + l / 8, LDS chunk position l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7).
   const int lrow = lane >> 3;
   const int lpos = lane & 7;
   auto issue = [&](int kt, float *da, float *db) {
@@ -81,7 +82,7 @@ linear_kernel(LinearLaunch a) {
     for (int p = 0; p < LPW; p++) {
       const int g = NW * p + wave;
       const int r = 8 * g + lrow;
-      int kc = kt + 4 * (lpos ^ (r & 7));
+      int kc = kt + 4 * (lpos ^ ((r >> 1) & 7));
       kc = kc < ke ? kc : kb;  // past the slice: a valid address, zeroed at use
       const int xr = min(m0 + r, a.m - 1);
       const int wr = min(n0 + r, a.n - 1);
@@ -104,12 +105,12 @@ linear_kernel(LinearLaunch a) {
 #pragma unroll
       for (int b = 0; b < MB; b++) {
         const int ra = wm * 32 * MB + b * 32 + i;
-        av[b] = ld4(sa + ra * BK + 4 * (c ^ (ra & 7)));
+        av[b] = ld4(sa + ra * BK + 4 * (c ^ ((ra >> 1) & 7)));
       }
 #pragma unroll
       for (int b = 0; b < 2; b++) {
         const int rb = wn * 64 + b * 32 + i;
-        bv[b] = ld4(sb + rb * BK + 4 * (c ^ (rb & 7)));
+        bv[b] = ld4(sb + rb * BK + 4 * (c ^ ((rb >> 1) & 7)));
       }
       if (!full && !(kt + 4 * c < ke)) {
 #pragma unroll

@@ -17,7 +17,7 @@
 //   * Key tiles of 32 rows of K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
 //     register staging), double-buffered so the next tile streams in while this one is used;
 //     one barrier per tile.  Rows are stored unpadded; K rows have their 16-byte chunks
-//     XOR-swizzled by (row & 7) so the column reads of QK are conflict-free, V rows are read
+//     XOR-swizzled (kswz) so the column reads of QK are conflict-free, V rows are read
 //     along the row and need no swizzle.  The block ids of the segment's pages are staged in LDS
 //     once, so a paged tile load never waits on a global table read.
 //   * Per tile each wave computes (D = 128)
@@ -81,6 +81,19 @@ __device__ __forceinline__ float sum4_lanes(float x) {
   return q.a + q.b;
 }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+
+// LDS position of chunk c of K row r (and, being an involution, the chunk at position c):
+// the low three bits are XORed with r & 7; from d = 256 on, where a lane group's chunks span a
+// whole 256-byte bank period, bit 3 is also XORed with the parity of the chunk's lane group.
+// Measured with SQ_LDS_BANK_CONFLICT: zero conflicts for d = 128, 256 and 512 (r & 15 alone:
+// 33% of the LDS-active cycles at d = 128).
+template <int D>
+__device__ __forceinline__ int kswz(int c, int r) {
+  constexpr int GS = D / 16;  // chunks per lane group
+  int x = r & 7;
+  if constexpr (GS >= 16) x |= ((c / GS) & 1) << 3;
+  return c ^ x;
+}
 
 // Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the block
 // table, which starts at page blk0.
@@ -210,9 +223,9 @@ prefill_kernel(TileLaunch a) {
       }
       const int key = min(kt + r, it.ke - 1);  // rows past the chunk are loaded but masked
       const int64_t row = tile_row(a.kv, stab, blk0, it.kbase, key);
-      // K chunks are XOR-swizzled by (row & 7) for the column reads of QK; V rows are read
+      // K chunks are XOR-swizzled (kswz) for the column reads of QK; V rows are read
       // along the row, which is conflict-free unswizzled.
-      const float *gk = kbase + row * rs + (pos ^ (r & 7)) * 4;
+      const float *gk = kbase + row * rs + kswz<D>(pos, r) * 4;
       const float *gv = vbase + row * rs + pos * 4;
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void *)gk,
@@ -228,7 +241,7 @@ prefill_kernel(TileLaunch a) {
     const bool full = (kt + KT <= whi_min) && (kt >= wlo_max);
 
     // S^T = K Q^T per 16-key block kb: A[key][k] = K[16kb + i][DQ*g + s] (lane i, g),
-    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at position c ^ (i & 7).  Chunk
+    // B[k][query] = qr[s].  Chunk c = (DQ/4)*g + j of row 16kb+i sits at kswz(c, i).  Chunk
     // j of every block is read at once, so each LDS wait is followed by 4 * KB MFMAs that
     // alternate between the blocks' accumulators.
     f32x4 st[KB];
@@ -236,7 +249,7 @@ prefill_kernel(TileLaunch a) {
     for (int blk = 0; blk < KB; blk++) st[blk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const float *kb[DQ / 4];
 #pragma unroll
-    for (int j = 0; j < DQ / 4; j++) kb[j] = sk + i * D + 4 * (((DQ / 4) * g + j) ^ (i & 7));
+    for (int j = 0; j < DQ / 4; j++) kb[j] = sk + i * D + 4 * kswz<D>((DQ / 4) * g + j, i);
 #pragma unroll
     for (int s = 0; s < DQ; s += 4) {
       float4 kk[KB];
