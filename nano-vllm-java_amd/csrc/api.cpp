@@ -501,21 +501,28 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   // the 256-row, 1.8 M-key decode, 4096-key items run the kernel at 7.0 TB/s against 6.9 TB/s
   // at 1024 (fewer partials to write and merge) and 6.96 / 6.84 TB/s at 8192 / 16384 (a
   // longer tail).
+  // When even 64-key items leave fewer than 8 workgroups per CU (a small step), the largest
+  // chunk that still gives 2 per CU is taken instead: short items then cost more in fixed
+  // per-workgroup work and partials than they add in parallelism (Gemma3 global decode,
+  // 32 rows, 202 MB: 64.3 against 70.5 us for decode plus merge; C1 and the Gemma3 local
+  // layer keep 64).
   int64_t total = 0;
   for (const Row &r : rows) total += std::max(0, r.kend - r.kbeg);
-  const int64_t target = (int64_t)ctx->num_cus * 8;
-  int chunk = 64;
-  for (int c = 4096; c >= 64; c >>= 1) {
+  auto items_at = [&](int c) {
     int64_t items = 0;
     for (const Row &r : rows) {
       const int len = r.kend - r.kbeg;
       if (len > 0) items += (len + c - 1) / c;
     }
-    if (items * key.wg_per_item >= target) {
-      chunk = c;
-      break;
-    }
+    return items * key.wg_per_item;
+  };
+  int chunk = 0;
+  for (int per_cu : {8, 2}) {
+    for (int c = 4096; c >= 64 && !chunk; c >>= 1)
+      if (items_at(c) >= (int64_t)ctx->num_cus * per_cu) chunk = c;
+    if (chunk) break;
   }
+  if (!chunk) chunk = 64;
   // A paged item of `chunk` keys spans at most (chunk - 1) / BS + 2 pages; the row kernel
   // stages at most kRowTablePages of them.
   if (key.paged) chunk = std::min(chunk, (kRowTablePages - 1) * key.block_size);
