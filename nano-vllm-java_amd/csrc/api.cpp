@@ -175,6 +175,10 @@ struct nva_ctx {
   DevBuf d_lin;      // split-K partial sums of the linear kernel
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
 
+  // Prefill occupancy (resident workgroups per CU) by (head dim, heads per workgroup), queried
+  // once on this context's device.
+  std::map<int, int> occupancy;
+
   bool timing = false;
   std::vector<PendingTiming> pending;
   std::vector<hipEvent_t> event_pool;
@@ -225,6 +229,30 @@ nva_status hip_fail(nva_ctx *ctx, hipError_t e, const char *what) {
   } while (0)
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Makes the context's device current for the scope of an entry point (its grow-only buffers
+// are allocated, and its occupancy queried, on that device) and restores the caller's.
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != device) (void)hipSetDevice(device);
+  }
+  explicit DeviceGuard(const nva_ctx *ctx) : DeviceGuard(ctx->device) {}
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+int ctx_prefill_blocks_per_cu(nva_ctx *ctx, int head_dim, int hpw) {
+  const int key = head_dim * 16 + hpw;
+  auto it = ctx->occupancy.find(key);
+  if (it != ctx->occupancy.end()) return it->second;
+  const int n = prefill_blocks_per_cu(head_dim, hpw);
+  ctx->occupancy[key] = n;
+  return n;
+}
 
 hipEvent_t take_event(nva_ctx *ctx) {
   if (!ctx->event_pool.empty()) {
@@ -642,7 +670,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   key.mfma = mfma ? 1 : 0;
   key.tile_q = mfma ? prefill_tile_queries(d.head_dim, hpw_tile) : 0;
   key.wg_per_item = d.num_kv_heads * (rep / hpw_row);
-  key.blocks_per_cu = mfma ? prefill_blocks_per_cu(d.head_dim, hpw_tile) : 0;
+  key.blocks_per_cu = mfma ? ctx_prefill_blocks_per_cu(ctx, d.head_dim, hpw_tile) : 0;
   key.tile_groups = mfma ? d.num_kv_heads * (rep / hpw_tile) : 0;
   key.tokens = num_tokens;
   key.paged = view.paged;
@@ -903,7 +931,9 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return NVA_E_HIP;
   if (device < 0 || device >= n) return NVA_E_ARG;
-  if (hipSetDevice(device) != hipSuccess) return NVA_E_HIP;
+  DeviceGuard dg(device);
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != device) return NVA_E_HIP;
   nva_ctx *ctx = new nva_ctx();
   ctx->device = device;
   hipDeviceProp_t prop;
@@ -931,7 +961,7 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
 
 nva_status nva_ctx_destroy(nva_ctx *ctx) {
   if (!ctx) return NVA_OK;
-  (void)hipSetDevice(ctx->device);
+  DeviceGuard dg(ctx);
   (void)hipStreamSynchronize(ctx->stream);
   (void)hipStreamSynchronize(ctx->side_stream);
   resolve_timings(ctx);
@@ -1002,6 +1032,7 @@ nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block
                          int num_kv_heads, const int32_t *head_dims, const uint8_t *allocate,
                          nva_kv **out) {
   if (!ctx || !out) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   *out = nullptr;
   if (num_layers <= 0) return fail(ctx, NVA_E_ARG, "numLayers must be > 0");
   if (num_blocks <= 0) return fail(ctx, NVA_E_ARG, "numBlocks must be > 0");
@@ -1017,7 +1048,6 @@ nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block
   kv->k.assign(num_layers, nullptr);
   kv->v.assign(num_layers, nullptr);
   kv->bytes.assign(num_layers, 0);
-  (void)hipSetDevice(ctx->device);
   for (int i = 0; i < num_layers; i++) {
     if (allocate && !allocate[i]) continue;
     if (head_dims[i] <= 0) {
@@ -1072,6 +1102,7 @@ static nva_status kv_copy(nva_kv *kv, int layer, int which, int64_t off, void *h
                           int64_t count, bool to_device) {
   if (!kv || !host || count < 0 || off < 0 || (which != 0 && which != 1)) return NVA_E_ARG;
   nva_ctx *ctx = kv->ctx;
+  DeviceGuard dg(ctx);
   if (layer < 0 || layer >= kv->num_layers)
     return fail(ctx, NVA_E_LAYER, "layerIndex out of range: %d (layers=%d)", layer,
                 kv->num_layers);
@@ -1103,6 +1134,7 @@ nva_status nva_kv_read(nva_kv *kv, int layer, int which, int64_t float_offset, f
 nva_status nva_rope_create(nva_ctx *ctx, const float *cos_sin, int max_pos, int head_size,
                            nva_rope **out) {
   if (!ctx || !out || !cos_sin) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   *out = nullptr;
   if (max_pos <= 0 || head_size <= 0 || head_size % 2)
     return fail(ctx, NVA_E_ARG, "RoPE table needs maxPos > 0 and an even headSize");
@@ -1161,6 +1193,7 @@ nva_status nva_step_set(nva_ctx *ctx, int is_prefill, const int32_t *cu_q, const
                         int bt_stride, const int32_t *seq_ids, const float *positions,
                         int num_tokens) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   if (num_seqs < 0 || num_slots < 0 || num_tokens < 0 || bt_stride < 0)
     return fail(ctx, NVA_E_ARG, "negative count in step metadata");
   if (is_prefill && !cu_q) return fail(ctx, NVA_E_ARG, "prefill step needs cuSeqlensQ");
@@ -1218,7 +1251,6 @@ nva_status nva_step_set(nva_ctx *ctx, int is_prefill, const int32_t *cu_q, const
   ctx->off_pos = off;
   off = align(off + ctx->pos.size() * 4);
   const size_t bytes = std::max<size_t>(off, 16);
-  (void)hipSetDevice(ctx->device);
   HIP_TRY(ctx, ctx->step_stage.reserve(bytes), "step staging");
   HIP_TRY(ctx, ctx->d_step.reserve(bytes), "step buffer");
   char *h = static_cast<char *>(ctx->step_stage.ptr);
@@ -1237,6 +1269,7 @@ nva_status nva_step_set(nva_ctx *ctx, int is_prefill, const int32_t *cu_q, const
 
 nva_status nva_step_positions(nva_ctx *ctx, const float *positions, int num_tokens) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   if (!ctx->has_step) return fail(ctx, NVA_E_NO_STEP, "no step metadata set on the context");
   if (num_tokens < 0 || (num_tokens > 0 && !positions))
     return fail(ctx, NVA_E_ARG, "positions required");
@@ -1280,6 +1313,7 @@ nva_status nva_step_clear(nva_ctx *ctx) {
 nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, const float *k,
                             int num_tokens, int hq, int hk, float *q_out, float *k_out) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   if (!rope) return fail(ctx, NVA_E_ARG, "RoPE table is null");
   if (!ctx->has_step) return fail(ctx, NVA_E_NO_STEP, "no step metadata set on the context");
   if (num_tokens < 0 || hq < 0 || hk < 0) return fail(ctx, NVA_E_ARG, "negative shape");
@@ -1314,6 +1348,7 @@ nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *
                                  const float *q, const float *k, const float *v, int num_tokens,
                                  float *out) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   nva_status st = check_forward(ctx, kv, desc, num_tokens);
   if (st != NVA_OK) return st;
   if (num_tokens == 0) return NVA_OK;  // empty batch: an empty output, as Tensor.zeros(0, ...)
@@ -1364,6 +1399,7 @@ static nva_status norm_rope_attention(nva_ctx *ctx, nva_kv *kv, const nva_rope *
                                       int k_ld, int v_ld, int num_tokens, float *q_out,
                                       float *k_out, float *out) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   nva_status st = check_forward(ctx, kv, desc, num_tokens);
   if (st != NVA_OK) return st;
   if (!rope) return fail(ctx, NVA_E_ARG, "RoPE table is null");
@@ -1481,6 +1517,7 @@ nva_status nva_qkv_norm_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const n
 nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
                               const float *weight, int out, const float *bias, float *y) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   if (rows < 0 || in <= 0 || out <= 0)
     return fail(ctx, NVA_E_ARG, "bad linear shape rows=%d in=%d out=%d", rows, in, out);
   if (rows == 0) return NVA_OK;
@@ -1559,6 +1596,7 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
 nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const float *x, int rows,
                                 int width, float *out) {
   if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
   if (!norm) return fail(ctx, NVA_E_ARG, "RMSNorm descriptor is null");
   if (rows < 0 || width <= 0) return fail(ctx, NVA_E_ARG, "bad shape [%d, %d]", rows, width);
   if (rows > 0 && (!x || !out)) return fail(ctx, NVA_E_ARG, "x and out are required");

@@ -167,7 +167,8 @@ bool row_kernel_supports(int head_dim, int heads_per_wg);
 // Most query heads one row-kernel workgroup carries at this head dim (register budget).
 int row_kernel_max_heads(int head_dim);
 bool prefill_kernel_supports(int head_dim, int heads_per_wg);
-// Prefill workgroups that can be resident on one CU at once (occupancy of the kernel).
+// Prefill workgroups that can be resident on one CU at once (occupancy of the kernel), queried
+// on the current device each call (callers cache it per device).
 int prefill_blocks_per_cu(int head_dim, int heads_per_wg);
 
 // Most pages one prefill key chunk may span (its block ids are staged in LDS).

@@ -418,19 +418,17 @@ bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
 
 namespace {
 
+// Uncached: the caller (one context per device) keeps the answer.  The query reads the
+// current device's properties, so the caller makes its device current first.
 template <int D, int HPW>
 int blocks_per_cu() {
-  static int n = -1;
-  if (n < 0) {
-    constexpr int NW = tile_waves<D>();
-    int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &b, prefill_kernel<D, HPW, key_tile<D>(), NW>, 64 * NW, 0) != hipSuccess ||
-        b < 1)
-      b = 1;
-    n = b;
-  }
-  return n;
+  constexpr int NW = tile_waves<D>();
+  int b = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &b, prefill_kernel<D, HPW, key_tile<D>(), NW>, 64 * NW, 0) != hipSuccess ||
+      b < 1)
+    b = 1;
+  return b;
 }
 
 template <int D>

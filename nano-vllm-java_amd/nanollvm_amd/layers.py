@@ -162,7 +162,8 @@ class Context:
 
     def prepare_prefill(self, seqs, block_size: int) -> None:
         """Transformer.preparePrefill + Context.set (Transformer.java:342-418) in the library:
-        ``seqs`` are engine.Sequence objects with numCachedTokens / numScheduledTokens set."""
+        ``seqs`` are Sequence-like objects (engine/Sequence.java) with numCachedTokens /
+        numScheduledTokens set."""
         from .step import seq_array
         arr, keep = seq_array(seqs)
         _check(self._h, N.load().nva_step_prepare_prefill(self._h, arr, len(seqs), block_size),

@@ -1,5 +1,5 @@
 """Step-metadata producers of libnva.so (include/nva.h: nva_build_prefill_metadata,
-nva_build_decode_metadata) over the engine's ``Sequence`` objects.
+nva_build_decode_metadata) over the engine's scheduled sequences.
 
 They restate Transformer.preparePrefill / prepareDecode (engine/Transformer.java:319-456) in the
 library's C++ host code, so a model runner hands the scheduled sequences over once per step.
@@ -10,12 +10,35 @@ build and upload in one call.
 from __future__ import annotations
 
 import ctypes
-from typing import List, Sequence
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
 
 import numpy as np
 
 from . import _native as N
-from .engine import StepMeta
+
+
+@dataclass
+class StepMeta:
+    """Arguments of Context.set plus the step's positions (Transformer.java:342-457)."""
+
+    is_prefill: bool
+    cu_seqlens_q: Optional[np.ndarray]
+    cu_seqlens_k: Optional[np.ndarray]
+    max_seqlen_q: int
+    max_seqlen_k: int
+    slot_mapping: Optional[np.ndarray]
+    context_lens: Optional[np.ndarray]
+    block_tables: Optional[np.ndarray]
+    seq_ids: np.ndarray
+    positions: np.ndarray
+
+    def context_args(self) -> dict:
+        return dict(is_prefill=self.is_prefill, cu_seqlens_q=self.cu_seqlens_q,
+                    cu_seqlens_k=self.cu_seqlens_k, max_seqlen_q=self.max_seqlen_q,
+                    max_seqlen_k=self.max_seqlen_k, slot_mapping=self.slot_mapping,
+                    context_lens=self.context_lens, block_tables=self.block_tables,
+                    seq_ids=self.seq_ids, positions=self.positions)
 
 
 class MetadataError(ValueError):
@@ -23,8 +46,9 @@ class MetadataError(ValueError):
 
 
 def seq_array(seqs: Sequence) -> tuple:
-    """nva_seq[] for ``seqs`` (engine.Sequence objects); the second item keeps the block-table
-    arrays alive while the first is in use."""
+    """nva_seq[] for ``seqs`` (objects with seq_id, num_tokens, num_cached_tokens,
+    num_scheduled_tokens and block_table, as engine/Sequence.java); the second item keeps the
+    block-table arrays alive while the first is in use."""
     arr = (N.Seq * max(1, len(seqs)))()
     keep: List[np.ndarray] = []
     for i, s in enumerate(seqs):
@@ -65,10 +89,10 @@ def _build(seqs, block_size: int, prefill: bool) -> StepMeta:
 
 
 def build_prefill_metadata(seqs, block_size: int) -> StepMeta:
-    """nva_build_prefill_metadata (Transformer.preparePrefill) over engine.Sequence objects."""
+    """nva_build_prefill_metadata (Transformer.preparePrefill) over Sequence-like objects."""
     return _build(seqs, block_size, True)
 
 
 def build_decode_metadata(seqs, block_size: int) -> StepMeta:
-    """nva_build_decode_metadata (Transformer.prepareDecode) over engine.Sequence objects."""
+    """nva_build_decode_metadata (Transformer.prepareDecode) over Sequence-like objects."""
     return _build(seqs, block_size, False)

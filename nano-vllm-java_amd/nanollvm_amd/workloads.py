@@ -31,7 +31,7 @@ from typing import List, Optional, Tuple
 
 import numpy as np
 
-from .engine import StepMeta
+from .step import StepMeta
 
 BLOCK_SIZE = 256
 POOL_CAP = 8191

@@ -1,8 +1,8 @@
 """Host-side producers of the step metadata the attention boundary consumes.
 
 These stay on the engine side of the boundary (in the reference they are Java and are not
-replaced); they are restated here so that tests and the benchmark can drive the library with
-exactly the metadata the reference's engine would hand it:
+replaced); they are restated here, as test infrastructure, so that the tests can drive the
+library with exactly the block ids and metadata the reference's engine would hand it:
 
 * ``Sequence``       -- engine/Sequence.java:323-361 (numBlocks, lastBlockNumTokens, block).
 * ``BlockManager``   -- engine/BlockManager.java:77-266 (paged allocator, prefix-cache hashing:
@@ -23,6 +23,8 @@ from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
 import numpy as np
+
+from nanollvm_amd.step import StepMeta
 
 _MASK64 = (1 << 64) - 1
 _FNV_OFFSET = 0xCBF29CE484222325
@@ -185,29 +187,6 @@ class BlockManager:
             blk.hash = h
             blk.token_ids = list(toks)
             self.hash_to_block[h] = blk.block_id
-
-
-@dataclass
-class StepMeta:
-    """Arguments of Context.set plus the step's positions (Transformer.java:342-457)."""
-
-    is_prefill: bool
-    cu_seqlens_q: Optional[np.ndarray]
-    cu_seqlens_k: Optional[np.ndarray]
-    max_seqlen_q: int
-    max_seqlen_k: int
-    slot_mapping: Optional[np.ndarray]
-    context_lens: Optional[np.ndarray]
-    block_tables: Optional[np.ndarray]
-    seq_ids: np.ndarray
-    positions: np.ndarray
-
-    def context_args(self) -> dict:
-        return dict(is_prefill=self.is_prefill, cu_seqlens_q=self.cu_seqlens_q,
-                    cu_seqlens_k=self.cu_seqlens_k, max_seqlen_q=self.max_seqlen_q,
-                    max_seqlen_k=self.max_seqlen_k, slot_mapping=self.slot_mapping,
-                    context_lens=self.context_lens, block_tables=self.block_tables,
-                    seq_ids=self.seq_ids, positions=self.positions)
 
 
 def prepare_block_tables(tables: List[List[int]]) -> np.ndarray:

@@ -3,7 +3,7 @@ test and the invariants the attention kernels rely on."""
 
 import numpy as np
 
-from nanollvm_amd import engine as E
+import engine as E
 from nanollvm_amd import workloads as W
 
 

@@ -10,7 +10,7 @@ import torch
 
 from cases import rel_l2
 from nanollvm_amd import Attention, Context, KvCacheArena
-from nanollvm_amd import engine as E
+import engine as E
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu

@@ -7,7 +7,7 @@ page.  Host only: no GPU."""
 import numpy as np
 import pytest
 
-from nanollvm_amd import engine as E
+import engine as E
 from nanollvm_amd import step as S
 
 
