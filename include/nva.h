@@ -94,7 +94,8 @@ const char *nva_status_string(nva_status status);
 /* Per-kernel timing with HIP events on the context's stream (off by default).  Kernel names:
  * "rope_store", "store", "decode", "merge", "prefill", "gather", "linear", "rms_norm";
  * "attention" spans the attention kernels of one call (decode and prefill kernels that
- * overlap count once). */
+ * overlap count once).  The name "device_bytes" instead returns in *launches the bytes of
+ * device memory the context's grow-only work buffers hold (arenas and RoPE tables excluded). */
 nva_status nva_ctx_set_timing(nva_ctx *ctx, int enable);
 nva_status nva_ctx_kernel_stats(nva_ctx *ctx, const char *kernel, int64_t *launches,
                                 double *total_ms);
@@ -231,6 +232,24 @@ nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, 
 nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
                                  const float *q, const float *k, const float *v, int num_tokens,
                                  float *out);
+
+/* nva_attention_forward without any allocation.  It has no counterpart in the reference: it is
+ * for callers that cannot allocate device memory while they run attention (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * semantics and kernels as nva_attention_forward, and bit-identical results; the plan lists,
+ * split partials and shared-KV gather rows go into a static device array of this library
+ * (NVA_NOALLOC_SCRATCH_BYTES = 128 MiB, one per device, held until the process ends) instead of
+ * the context's grow-only buffers, and the call makes no hipMalloc, hipFree or other allocating
+ * call.  A step whose plan, partials and gathered rows need more than that fails with NVA_E_ARG
+ * and a message giving the bytes needed.  Every call on a device shares that device's array and
+ * it keeps the last call's contents: calls that overlap on one device (several host threads or
+ * contexts, or streams not ordered with each other) race and must be serialised by the caller.
+ * The step metadata still comes from nva_step_set(), whose buffers grow (allocate) when a step
+ * is larger than every earlier one on the context. */
+#define NVA_NOALLOC_SCRATCH_BYTES (128u << 20)
+nva_status nva_attention_forward_noalloc(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
+                                         const float *q, const float *k, const float *v,
+                                         int num_tokens, float *out);
 
 /* The pair RotaryEmbedding.forward + Attention.forward as one call, the way the model layers
  * use them (models/internal/Qwen3ForCausalLM.java:207-222): one fused kernel rotates q and k

@@ -12,11 +12,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -25,7 +27,60 @@
 
 using namespace nva;
 
+// Device scratch of nva_attention_forward_noalloc: the plan lists, split partials and shared-KV
+// gather rows of one call.  One copy per device, held from the library's load on that device
+// until the process ends.  Host code never uses the name `scratch` as an address (on the host it
+// is only a stand-in for the symbol): nva_ctx_create looks up each device's address once with
+// hipGetSymbolAddress, and every later use goes through that address.  Nothing in it has to
+// start at zero: every partial is written before the merge reads it, and the plan lists and
+// gather rows are written by the call that reads them.
 namespace {
+constexpr size_t kScratchBytes = NVA_NOALLOC_SCRATCH_BYTES;
+constexpr int kScratchDevices = 64;
+}  // namespace
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+// The scratch plan held by one device's array, so a call can skip copying the same plan again.
+struct ScratchTag {
+  uint64_t plan_id = 0;
+  size_t offset = 0;
+};
+
+// Per device: its address of `scratch` (looked up once, under the mutex, with that device
+// current) and the tag of the plan it holds.
+struct ScratchSlot {
+  bool looked_up = false;
+  hipError_t err = hipSuccess;
+  char *ptr = nullptr;
+  ScratchTag tag;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kScratchDevices];
+
+// Called by nva_ctx_create with `device` current.
+char *scratch_address(int device, hipError_t *err) {
+  if (device < 0 || device >= kScratchDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot &slot = g_scratch[device];
+  if (!slot.looked_up) {
+    void *p = nullptr;
+    slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    slot.ptr = slot.err == hipSuccess ? static_cast<char *>(p) : nullptr;
+    slot.looked_up = true;
+  }
+  *err = slot.err;
+  return slot.ptr;
+}
+
+ScratchTag &scratch_tag(int device) { return g_scratch[device].tag; }
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 
 // Grow-only device buffer.
 struct DevBuf {
@@ -126,8 +181,20 @@ struct Plan {
   int max_parts = 0;  // most partials any merged row has
   bool covers_all = true;  // every output row is written by some kernel
   size_t off_rows = 0, off_merge = 0, off_tiles = 0, off_slots = 0;
+  std::vector<char> host;  // the packed lists at the offsets above
+  uint64_t id = 0;         // unique per build (identifies the plan held in a scratch array)
+  bool on_device = false;  // host bytes uploaded to dev
   DevBuf dev;
   Staging stage;
+};
+
+// Workspace of the no-allocation entry point: the plan, the split partials and the shared-KV
+// gather rows of one call live in fixed regions of a device's static scratch array instead of
+// the context's grow-only buffers.  base is that device's address of the array (from
+// hipGetSymbolAddress), used == bytes already taken (gather rows, at the front).
+struct Scratch {
+  char *base = nullptr;
+  size_t used = 0;
 };
 
 struct PendingTiming {
@@ -174,6 +241,10 @@ struct nva_ctx {
   DevBuf d_v_norm;   // fused path scratch for normalised v (dense prefill with a v norm)
   DevBuf d_lin;      // split-K partial sums of the linear kernel
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
+
+  // This device's address of the no-allocation scratch array (null if the lookup failed).
+  char *scratch = nullptr;
+  hipError_t scratch_err = hipSuccess;
 
   // Prefill occupancy (resident workgroups per CU) by (head dim, heads per workgroup), queried
   // once on this context's device.
@@ -344,7 +415,8 @@ struct Row {
   int qrow, seq, kbase, kbeg, kend;
 };
 
-// Builds (or reuses) the plan for this configuration of the current step.
+// Builds (or reuses) the host lists of the plan for this configuration of the current step;
+// upload_plan() or the scratch path puts them on the device.
 nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   for (Plan *p : ctx->plans)
     if (p->valid && p->key == key) {
@@ -608,21 +680,31 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   plan->off_merge = plan->off_rows + items.size() * sizeof(RowItem);
   plan->off_tiles = plan->off_merge + merges.size() * sizeof(MergeItem);
   plan->off_slots = plan->off_tiles + tiles.size() * sizeof(TileItem);
-  const size_t bytes = plan->off_slots + seg_off.size() * sizeof(int32_t);
-  if (bytes > 0) {
-    HIP_TRY(ctx, plan->stage.reserve(bytes), "plan staging");
-    HIP_TRY(ctx, plan->dev.reserve(bytes), "plan buffer");
-    char *h = static_cast<char *>(plan->stage.ptr);
-    if (!items.empty()) memcpy(h + plan->off_rows, items.data(), items.size() * sizeof(RowItem));
-    if (!merges.empty())
-      memcpy(h + plan->off_merge, merges.data(), merges.size() * sizeof(MergeItem));
-    if (!tiles.empty()) memcpy(h + plan->off_tiles, tiles.data(), tiles.size() * sizeof(TileItem));
-    if (!seg_off.empty())
-      memcpy(h + plan->off_slots, seg_off.data(), seg_off.size() * sizeof(int32_t));
-    HIP_TRY(ctx, plan->stage.upload(plan->dev, bytes, ctx->stream), "plan upload");
-  }
+  plan->host.resize(plan->off_slots + seg_off.size() * sizeof(int32_t));
+  char *h = plan->host.data();
+  if (!items.empty()) memcpy(h + plan->off_rows, items.data(), items.size() * sizeof(RowItem));
+  if (!merges.empty())
+    memcpy(h + plan->off_merge, merges.data(), merges.size() * sizeof(MergeItem));
+  if (!tiles.empty()) memcpy(h + plan->off_tiles, tiles.data(), tiles.size() * sizeof(TileItem));
+  if (!seg_off.empty())
+    memcpy(h + plan->off_slots, seg_off.data(), seg_off.size() * sizeof(int32_t));
+  static std::atomic<uint64_t> next_id{1};
+  plan->id = next_id.fetch_add(1);
+  plan->on_device = false;
   plan->valid = true;
   *out = plan;
+  return NVA_OK;
+}
+
+// The plan's lists in the context's device buffer (uploaded once per plan).
+nva_status upload_plan(nva_ctx *ctx, Plan *plan) {
+  const size_t bytes = plan->host.size();
+  if (plan->on_device || bytes == 0) return NVA_OK;
+  HIP_TRY(ctx, plan->stage.reserve(bytes), "plan staging");
+  HIP_TRY(ctx, plan->dev.reserve(bytes), "plan buffer");
+  memcpy(plan->stage.ptr, plan->host.data(), bytes);
+  HIP_TRY(ctx, plan->stage.upload(plan->dev, bytes, ctx->stream), "plan upload");
+  plan->on_device = true;
   return NVA_OK;
 }
 
@@ -650,9 +732,11 @@ KvView make_dense_view(const float *k, const float *v) {
   return view;
 }
 
-// The attention part of Attention.forward once the store (if any) is done.
+// The attention part of Attention.forward once the store (if any) is done.  With scr null the
+// plan and partials use the context's buffers; otherwise the scratch array's regions.
 nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &view,
-                         int num_blocks, const float *q, int num_tokens, float *out) {
+                         int num_blocks, const float *q, int num_tokens, float *out,
+                         Scratch *scr) {
   const int rep = d.num_heads / d.num_kv_heads;
   const int hpw_row = largest_pow2_divisor_upto(rep, row_kernel_max_heads(d.head_dim));
   // Query heads per prefill workgroup: at most a quarter of its waves, so a workgroup covers at
@@ -683,6 +767,39 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   nva_status st = get_plan(ctx, key, &plan);
   if (st != NVA_OK) return st;
 
+  const size_t parts = (size_t)plan->num_parts * d.num_heads;
+  const size_t part_bytes = parts * (2 + (size_t)d.head_dim) * sizeof(float);
+  char *pbase = nullptr;
+  float *pm = nullptr;
+  if (!scr) {
+    st = upload_plan(ctx, plan);
+    if (st != NVA_OK) return st;
+    pbase = static_cast<char *>(plan->dev.ptr);
+    if (parts > 0) HIP_TRY(ctx, ctx->d_part.reserve(part_bytes), "partial buffer");
+    pm = static_cast<float *>(ctx->d_part.ptr);
+  } else {
+    // Regions after the gather rows: [plan lists | partials], 256-byte aligned.
+    const size_t plan_off = align256(scr->used);
+    const size_t part_off = align256(plan_off + plan->host.size());
+    if (part_off + part_bytes > kScratchBytes)
+      return fail(ctx, NVA_E_ARG,
+                  "this call needs %zu bytes of device scratch (plan %zu, partials %zu, gather "
+                  "%zu); the no-allocation entry point has %zu",
+                  part_off + part_bytes, plan->host.size(), part_bytes, scr->used,
+                  kScratchBytes);
+    pbase = scr->base + plan_off;
+    pm = reinterpret_cast<float *>(scr->base + part_off);
+    // Skip the copy when this device's array already holds this very plan at this offset.
+    ScratchTag &tag = scratch_tag(ctx->device);
+    if (!plan->host.empty() && (tag.plan_id != plan->id || tag.offset != plan_off)) {
+      HIP_TRY(ctx, hipMemcpyAsync(pbase, plan->host.data(), plan->host.size(),
+                                  hipMemcpyHostToDevice, ctx->stream),
+              "plan copy to scratch");
+      tag.plan_id = plan->id;
+      tag.offset = plan_off;
+    }
+  }
+
   // "attention" times the whole part below, kernels that overlap counted once.
   Timed span(ctx, "attention");
   if (!plan->covers_all) {
@@ -690,13 +807,6 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     HIP_TRY(ctx, launch_zero(out, (size_t)num_tokens * d.num_heads * d.head_dim, ctx->stream),
             "zero output");
   }
-  char *pbase = static_cast<char *>(plan->dev.ptr);
-  const size_t parts = (size_t)plan->num_parts * d.num_heads;
-  if (parts > 0) {
-    const size_t need = parts * (2 + (size_t)d.head_dim) * sizeof(float);
-    HIP_TRY(ctx, ctx->d_part.reserve(need), "partial buffer");
-  }
-  float *pm = static_cast<float *>(ctx->d_part.ptr);
   // A mixed step (MFMA tiles and rows in one plan) runs the HBM-bound rows on the side stream
   // while the MFMA-bound tiles run on the main stream; both write disjoint partials, and the
   // main stream waits for the side stream before the merge.  The tiles are issued first: the
@@ -833,16 +943,17 @@ nva_status check_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc, in
   return NVA_OK;
 }
 
-// Which K/V the attention reads, Attention.java:161-170 and :176-195.
+// Which K/V the attention reads, Attention.java:161-170 and :176-195.  scr selects the
+// no-allocation workspace (null: the context's buffers).
 nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &d,
                                  const float *q, const float *k, const float *v,
-                                 int num_tokens, float *out) {
+                                 int num_tokens, float *out, Scratch *scr = nullptr) {
   const int layer = d.kv_layer_index;
   const bool allocated = kv->k[layer] != nullptr;
   if (ctx->is_prefill && !ctx->has_tables) {
     if (d.write_kv) {
       if (!k || !v) return fail(ctx, NVA_E_ARG, "dense prefill needs k and v");
-      return run_attention(ctx, d, make_dense_view(k, v), 0, q, num_tokens, out);
+      return run_attention(ctx, d, make_dense_view(k, v), 0, q, num_tokens, out, scr);
     }
     // Shared-KV dense prefill: gather the producer's rows at the step's slots.
     if (!ctx->has_slots || ctx->num_slots != num_tokens)
@@ -853,8 +964,20 @@ nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &
     nva_status sst = check_slots(ctx, kv);
     if (sst != NVA_OK) return sst;
     const size_t row = (size_t)d.num_kv_heads * d.head_dim;
-    HIP_TRY(ctx, ctx->d_gather.reserve(2 * (size_t)num_tokens * row * 4 + 16), "gather buffer");
-    float *gk = static_cast<float *>(ctx->d_gather.ptr);
+    const size_t gather_bytes = 2 * (size_t)num_tokens * row * 4 + 16;
+    float *gk = nullptr;
+    if (!scr) {
+      HIP_TRY(ctx, ctx->d_gather.reserve(gather_bytes), "gather buffer");
+      gk = static_cast<float *>(ctx->d_gather.ptr);
+    } else {
+      if (gather_bytes > kScratchBytes)
+        return fail(ctx, NVA_E_ARG,
+                    "this call's gathered K/V rows need %zu bytes of device scratch; the "
+                    "no-allocation entry point has %zu",
+                    gather_bytes, kScratchBytes);
+      gk = reinterpret_cast<float *>(scr->base);
+      scr->used = gather_bytes;
+    }
     float *gv = gk + (size_t)num_tokens * row;
     GatherLaunch g;
     g.k_cache = kv->k[layer];
@@ -867,12 +990,12 @@ nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &
     Timed tm(ctx, "gather");
     HIP_TRY(ctx, launch_gather(g, ctx->stream), "gather kernel launch");
     tm.done();
-    return run_attention(ctx, d, make_dense_view(gk, gv), 0, q, num_tokens, out);
+    return run_attention(ctx, d, make_dense_view(gk, gv), 0, q, num_tokens, out, scr);
   }
   if (!allocated) return fail(ctx, NVA_E_ARG, "layer %d has no pages to attend over", layer);
   if (!ctx->has_tables) return fail(ctx, NVA_E_ARG, "paged attention needs block tables");
   return run_attention(ctx, d, make_paged_view(ctx, kv, layer), kv->num_blocks, q,
-                       num_tokens, out);
+                       num_tokens, out, scr);
 }
 
 // The kernels' view of an RMSNorm descriptor; NULL disables the norm.  Any eps is accepted, as
@@ -955,6 +1078,7 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
     return NVA_E_HIP;
   }
   ctx->stream = ctx->own_stream;
+  ctx->scratch = scratch_address(device, &ctx->scratch_err);
   *out = ctx;
   return NVA_OK;
 }
@@ -1012,6 +1136,15 @@ nva_status nva_ctx_set_timing(nva_ctx *ctx, int enable) {
 nva_status nva_ctx_kernel_stats(nva_ctx *ctx, const char *kernel, int64_t *launches,
                                 double *total_ms) {
   if (!ctx || !kernel) return NVA_E_ARG;
+  if (strcmp(kernel, "device_bytes") == 0) {
+    // Device memory the context's grow-only buffers hold (not the arenas or RoPE tables).
+    size_t b = ctx->d_step.cap + ctx->d_part.cap + ctx->d_q_rot.cap + ctx->d_k_rot.cap +
+               ctx->d_v_norm.cap + ctx->d_lin.cap + ctx->d_gather.cap;
+    for (const Plan *p : ctx->plans) b += p->dev.cap;
+    if (launches) *launches = (int64_t)b;
+    if (total_ms) *total_ms = 0.0;
+    return NVA_OK;
+  }
   resolve_timings(ctx);
   auto it = ctx->stats.find(kernel);
   if (launches) *launches = it == ctx->stats.end() ? 0 : it->second.launches;
@@ -1344,11 +1477,11 @@ nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, 
   return NVA_OK;
 }
 
-nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
-                                 const float *q, const float *k, const float *v, int num_tokens,
-                                 float *out) {
-  if (!ctx) return NVA_E_ARG;
-  DeviceGuard dg(ctx);
+// Attention.forward: the store, then the attention kernels; scr selects the no-allocation
+// workspace (null: the context's buffers).
+static nva_status attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
+                                    const float *q, const float *k, const float *v,
+                                    int num_tokens, float *out, Scratch *scr) {
   nva_status st = check_forward(ctx, kv, desc, num_tokens);
   if (st != NVA_OK) return st;
   if (num_tokens == 0) return NVA_OK;  // empty batch: an empty output, as Tensor.zeros(0, ...)
@@ -1379,7 +1512,28 @@ nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *
     HIP_TRY(ctx, launch_rope_store(a, ctx->stream, ctx->num_cus), "store kernel launch");
     tm.done();
   }
-  return attention_after_store(ctx, kv, d, q, k, v, num_tokens, out);
+  return attention_after_store(ctx, kv, d, q, k, v, num_tokens, out, scr);
+}
+
+nva_status nva_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
+                                 const float *q, const float *k, const float *v, int num_tokens,
+                                 float *out) {
+  if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
+  return attention_forward(ctx, kv, desc, q, k, v, num_tokens, out, nullptr);
+}
+
+nva_status nva_attention_forward_noalloc(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc *desc,
+                                         const float *q, const float *k, const float *v,
+                                         int num_tokens, float *out) {
+  if (!ctx) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
+  if (!ctx->scratch)
+    return fail(ctx, NVA_E_HIP, "device scratch array unavailable on device %d: %s",
+                ctx->device, hipGetErrorString(ctx->scratch_err));
+  Scratch scr;
+  scr.base = ctx->scratch;
+  return attention_forward(ctx, kv, desc, q, k, v, num_tokens, out, &scr);
 }
 
 nva_status nva_rope_attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_rope *rope,

@@ -123,6 +123,8 @@ SIGNATURES = {
     "nva_step_clear": ([_vp], _st),
     "nva_rope_forward": ([_vp, _vp, _vp, _vp, _ci, _ci, _ci, _vp, _vp], _st),
     "nva_attention_forward": ([_vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci, _vp], _st),
+    "nva_attention_forward_noalloc": ([_vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci,
+                                       _vp], _st),
     "nva_rope_attention_forward": ([_vp, _vp, _vp, ctypes.POINTER(AttnDesc), _vp, _vp, _vp, _ci,
                                     _vp, _vp, _vp], _st),
     "nva_rms_norm_forward": ([_vp, _pnorm, _vp, _ci, _ci, _vp], _st),
