@@ -178,7 +178,7 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
     ms = (t1 - t0) * 1e3 / steps
     log(f"{label}: {ms:.4f} ms/step; kernels " + ", ".join(
         f"{n}={s[1] / max(s[0], 1):.4f}ms x{s[0]}" for n, s in stats.items() if s[0]))
-    return ms, stats
+    return ms, stats, time_step_plan(ctx, wl, step)
 
 
 def time_step_prepare(ctx, wl, reps=30):
@@ -211,6 +211,40 @@ def time_step_prepare(ctx, wl, reps=30):
     upload = 4 * (tokens * 2 + bt + 2 * (len(wl.seqs) + 1) + len(wl.seqs))
     return {"build_upload_us": round((t1 - t0) / reps * 1e6, 1), "sequences": len(wl.seqs),
             "tokens": tokens, "pages": pages, "upload_bytes": upload}
+
+
+def step_metadata(ctx, wl, plan):
+    """Per-step host cost: the metadata producer plus one upload, then the first layer's work
+    plan (build, upload); the sum is what a scheduler step pays once, before the kernels of its
+    first layer."""
+    out = time_step_prepare(ctx, wl)
+    out.update(plan)
+    out["per_step_host_us"] = round(out["build_upload_us"] + plan["plans_per_step"] *
+                                    (plan["plan_build_us"] + plan["plan_upload_us"]), 1)
+    return out
+
+
+def time_step_plan(ctx, wl, step, reps=20):
+    """Host cost of the work plan a scheduler step builds at its first layer (the library's own
+    host timer): after each nva_step_set the first attention call checks every page of the
+    step's tables, builds and sorts the work lists and uploads them; later layers reuse the
+    plan."""
+    import torch
+    args = wl.meta.context_args()
+    ctx.reset_stats()
+    ctx.set_timing(True)
+    for _ in range(reps):
+        ctx.set(**args)
+        step()
+        torch.cuda.synchronize()
+    ctx.set_timing(False)
+    nb, msb = ctx.kernel_stats("plan")
+    nu, msu = ctx.kernel_stats("plan_upload")
+    ctx.reset_stats()
+    build_us = msb / max(nb, 1) * 1e3
+    upload_us = msu / max(nu, 1) * 1e3
+    return {"plan_build_us": round(build_us, 1), "plan_upload_us": round(upload_us, 1),
+            "plans_per_step": round(nb / reps, 2)}
 
 
 def time_o_proj(ctx, attn_out, wl, steps, warmup, hidden=1024, seed=21):
@@ -275,8 +309,8 @@ def bench_decode(args, ctx):
     v = torch.randn((T, wl.hkv, wl.d), device="cuda", generator=g)
     oq = torch.empty_like(q)
     attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
-    ms, stats = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps, args.warmup,
-                          "decode")
+    ms, stats, plan = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps,
+                                args.warmup, "decode")
     byts = decode_bytes(wl)
     n_dec, t_dec = stats["decode"]
     dec_ms = t_dec / max(n_dec, 1)
@@ -290,7 +324,7 @@ def bench_decode(args, ctx):
                      "kernel": "row_attention_kernel<128,2> (split-KV decode)",
                      "algorithmic_bytes_per_launch": byts},
         "kernel_a": kernel_a_roofline(wl, stats),
-        "step_metadata": time_step_prepare(ctx, wl),
+        "step_metadata": step_metadata(ctx, wl, plan),
     }
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
@@ -319,8 +353,8 @@ def bench_prefill(args, ctx):
     oq = torch.empty_like(q)
     attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
     # Paged prefill reads rotated k from the pages, so the rotated k tensor is not requested.
-    ms, stats = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps, args.warmup,
-                          "prefill")
+    ms, stats, plan = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps,
+                                args.warmup, "prefill")
     flops = 4.0 * wl.d * wl.hq * wl.visible_pairs()
     n_pf, t_pf = stats["prefill"]
     pf_ms = t_pf / max(n_pf, 1)
@@ -337,7 +371,7 @@ def bench_prefill(args, ctx):
                      "kernel": "prefill_kernel<128,2> (fp32 MFMA 16x16x4, 8 waves)",
                      "algorithmic_flops_per_launch": flops},
         "kernel_a": kernel_a_roofline(wl, stats),
-        "step_metadata": time_step_prepare(ctx, wl),
+        "step_metadata": step_metadata(ctx, wl, plan),
     }
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
@@ -392,8 +426,8 @@ def bench_extra(args, ctx):
     attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
     junk = torch.empty(512 << 18, device="cuda") if args.flush else None
     flush = (lambda: junk.fill_(1.0)) if args.flush else None
-    ms, stats = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps, args.warmup,
-                          wl.name, flush=flush)
+    ms, stats, plan = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps,
+                                args.warmup, wl.name, flush=flush)
     dec_rows = [(c, n) for c, n in wl.seqs if n == 1]
     pf_rows = [(c, n) for c, n in wl.seqs if n > 1]
     dec_bytes = 0
@@ -420,71 +454,102 @@ def bench_extra(args, ctx):
                                 "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
     bound = max(dec_bytes / (HBM_PEAK_GBS * 1e9), flops / (FP32_MFMA_PEAK_TFLOPS * 1e12)) * 1e3
     line["lower_bound_ms"] = round(bound, 5)
+    line["step_metadata"] = step_metadata(ctx, wl, plan)
     line["attention_ms"] = round(kms.get("attention", 0.0), 5)
     rope.close()
     arena.close()
     return line
 
 
+def host_cpu():
+    """(model string, SIMD lanes of the JDK's FloatVector.SPECIES_PREFERRED on this host:
+    16 with AVX-512, 8 with AVX2, 4 otherwise) from /proc/cpuinfo."""
+    model, flags, fam = "", set(), {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and not model:
+                    model = val
+                elif key in ("cpu family", "model", "stepping", "vendor_id") and key not in fam:
+                    fam[key] = val
+                elif key == "flags" and not flags:
+                    flags = set(val.split())
+    except OSError:
+        pass
+    lanes = 16 if "avx512f" in flags else 8 if "avx2" in flags else 4
+    simd = "avx512f" if lanes == 16 else "avx2" if lanes == 8 else "sse"
+    desc = (f"{model} ({fam.get('vendor_id', '?')} family {fam.get('cpu family', '?')} model "
+            f"{fam.get('model', '?')} stepping {fam.get('stepping', '?')}, {simd})")
+    return desc, lanes
+
+
 def cpu_baseline(wl, budget_s):
-    """Times the oracle's Attention.forward (decode branch) on the host on the first rows of the
-    decode workload (at most 1024 pages of K/V), repeating it for about budget_s seconds."""
+    """The oracle's Attention.forward (decode branch) on the host cores, over the whole headline
+    decode step: the same 256 rows, contexts and block tables (page contents are a tiled
+    pattern; values do not change the work).  The oracle is built here for this host
+    (-O3 -march=native) and run with the reference's default float kernels, the Vector API
+    (FloatKernelsFactory "auto", FloatKernelsFactory.java:41-75) at the host's preferred lane
+    count, on every CPU this process may use (availableProcessors, LLM.java:1930-1944) and on
+    one thread.  The reference's decode splits each row's head-major jobs over the workers
+    (Attention.java:317-325, MatmulRuntime.java:194-225), so at most Hq threads work at once."""
+    import tempfile
+
     import numpy as np
     from oracle import oracle as O
-    from nanollvm_amd import workloads as W
 
-    threads = min(16, os.cpu_count() or 1)
-    rows, pages = 0, 0
-    for c, n in wl.seqs:
-        p = -(-(c + n) // wl.block_size)
-        if rows and pages + p > 1024:
-            break
-        rows, pages = rows + 1, pages + p
-    seqs = wl.seqs[:rows]
-    sub = W.build("cpu sample", seqs, is_prefill=False, hq=wl.hq, hkv=wl.hkv, d=wl.d,
-                  scale=wl.scale, rng=np.random.default_rng(0))
-    m = sub.meta
+    native = O.build_native(os.path.join(tempfile.mkdtemp(prefix="nva_cpu_"), "liboracle.so"))
+    O.set_library(native)
+    model, lanes = host_cpu()
+    affinity = len(os.sched_getaffinity(0))
+    threads = affinity
+    m = wl.meta
+    shape = (wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+    t_fill = time.perf_counter()
     rng = np.random.default_rng(5)
-    shape = (sub.num_blocks, sub.block_size, sub.hkv, sub.d)
-    block = rng.standard_normal(1 << 20, dtype=np.float32)
-    n = int(np.prod(shape))
-    kc = np.resize(block, n).reshape(shape)
-    vc = np.resize(block[::-1].copy(), n).reshape(shape)
-    q = rng.standard_normal((rows, sub.hq, sub.d), dtype=np.float32)
-    kv = rng.standard_normal((rows, sub.hkv, sub.d), dtype=np.float32)
+    block = rng.standard_normal(1 << 24, dtype=np.float32)
+    kc = np.empty(shape, np.float32)
+    vc = np.empty(shape, np.float32)
+    for arr, src in ((kc, block), (vc, block[::-1].copy())):
+        flat = arr.reshape(-1)
+        for s in range(0, flat.size, src.size):
+            e = min(flat.size, s + src.size)
+            flat[s:e] = src[: e - s]
+    rows = len(wl.seqs)
+    q = rng.standard_normal((rows, wl.hq, wl.d), dtype=np.float32)
+    kv = rng.standard_normal((rows, wl.hkv, wl.d), dtype=np.float32)
 
     def once(nthreads):
         t0 = time.perf_counter()
-        O.attention_forward(sub.hq, sub.d, sub.scale, sub.hkv, is_prefill=False, q=q, k=kv,
-                            v=kv, slot_mapping=m.slot_mapping, context_lens=m.context_lens,
+        O.attention_forward(wl.hq, wl.d, wl.scale, wl.hkv, is_prefill=False, q=q, k=kv, v=kv,
+                            slot_mapping=m.slot_mapping, context_lens=m.context_lens,
                             block_tables=m.block_tables, k_cache=kc, v_cache=vc,
-                            threads=nthreads)
+                            threads=nthreads, kernels=lanes)
         return time.perf_counter() - t0
 
-    byts = decode_bytes(sub)
-    toks = int(sum(c + n for c, n in seqs))
+    byts = decode_bytes(wl)
+    log(f"cpu baseline: {model}, {affinity} CPUs, {lanes} lanes, whole step "
+        f"({byts / 1e9:.2f} GB); pages filled in {time.perf_counter() - t_fill:.1f} s")
     dt1 = once(1)
     reps, spent = 0, 0.0
     while reps == 0 or spent < max(0.0, budget_s - dt1):
         spent += once(threads)
         reps += 1
     dt = spent / reps
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(byts / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+    busy = min(threads, wl.hq)
+    return {"value": round(byts / dt / 1e9, 3), "unit": "GB/s", "cores": busy,
             "kind": "port",
-            "sample": f"decode rows 0..{rows - 1} of the same workload ({toks} context tokens, "
-                      f"{pages} pages, {byts / 1e9:.2f} GB algorithmic per pass), oracle (C "
-                      f"restatement of Attention.attendJobs, scalar-kernel semantics), "
-                      f"{threads} threads with the reference's head-major split, mean of "
-                      f"{reps} passes of {dt:.3f} s",
-            "single_thread_gbs": round(byts / dt1 / 1e9, 3), "cpu_model": cpu_model}
+            "sample": f"the whole decode step ({rows} rows, "
+                      f"{int(sum(c + n for c, n in wl.seqs))} context tokens, "
+                      f"{byts / 1e9:.2f} GB algorithmic), oracle (C restatement of "
+                      f"Attention.attendJobs) built -O3 -march=native on this host, "
+                      f"VectorFloatKernels semantics at {lanes} lanes, the reference's "
+                      f"head-major job split over {threads} workers (at most {busy} busy: "
+                      f"{wl.hq} head jobs per row), mean of {reps} passes of {dt:.3f} s",
+            "single_thread": {"value": round(byts / dt1 / 1e9, 3), "seconds": round(dt1, 3)},
+            "threads": threads, "nproc": os.cpu_count(), "affinity_cpus": affinity,
+            "vector_lanes": lanes, "cpu_model": model}
 
 
 def main():

@@ -94,8 +94,10 @@ const char *nva_status_string(nva_status status);
 /* Per-kernel timing with HIP events on the context's stream (off by default).  Kernel names:
  * "rope_store", "store", "decode", "merge", "prefill", "gather", "linear", "rms_norm";
  * "attention" spans the attention kernels of one call (decode and prefill kernels that
- * overlap count once).  The name "device_bytes" instead returns in *launches the bytes of
- * device memory the context's grow-only work buffers hold (arenas and RoPE tables excluded). */
+ * overlap count once).  Host-side entries: "plan" (building a step's work plan on the host, once
+ * per step and attention configuration, at its first layer) and "plan_upload" (copying it to
+ * the device).  The name "device_bytes" instead returns in *launches the bytes of device memory
+ * the context's grow-only work buffers hold (arenas and RoPE tables excluded). */
 nva_status nva_ctx_set_timing(nva_ctx *ctx, int enable);
 nva_status nva_ctx_kernel_stats(nva_ctx *ctx, const char *kernel, int64_t *launches,
                                 double *total_ms);

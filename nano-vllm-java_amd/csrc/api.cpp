@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -374,6 +375,26 @@ void resolve_timings(nva_ctx *ctx) {
   ctx->pending.clear();
 }
 
+// Host time of one plan build (and its upload), kept as the "plan" entry of the kernel stats
+// when timing is on: the per-step planning cost a scheduler step pays at its first layer.
+struct HostTimed {
+  nva_ctx *ctx;
+  const char *name;
+  std::chrono::steady_clock::time_point t0;
+  bool on;
+  HostTimed(nva_ctx *c, const char *n) : ctx(c), name(n), on(c->timing) {
+    if (on) t0 = std::chrono::steady_clock::now();
+  }
+  ~HostTimed() {
+    if (!on) return;
+    const double ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    auto &s = ctx->stats[name];
+    s.launches++;
+    s.ms += ms;
+  }
+};
+
 int pow2_shift(int x) {
   if (x <= 0 || (x & (x - 1))) return -1;
   int s = 0;
@@ -423,6 +444,7 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
       *out = p;
       return NVA_OK;
     }
+  HostTimed host_timer(ctx, "plan");
   Plan *plan = nullptr;
   for (Plan *p : ctx->plans)
     if (!p->valid) {
@@ -700,6 +722,7 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
 nva_status upload_plan(nva_ctx *ctx, Plan *plan) {
   const size_t bytes = plan->host.size();
   if (plan->on_device || bytes == 0) return NVA_OK;
+  HostTimed host_timer(ctx, "plan_upload");
   HIP_TRY(ctx, plan->stage.reserve(bytes), "plan staging");
   HIP_TRY(ctx, plan->dev.reserve(bytes), "plan buffer");
   memcpy(plan->stage.ptr, plan->host.data(), bytes);

@@ -103,7 +103,7 @@ static float dot_scalar(const float *a, const float *b, int n) {
 /* VectorFloatKernels.dot with LANE lanes: four FMA accumulators, (acc0+acc1)+(acc2+acc3),
  * lane reduction, scalar tail (VectorFloatKernels.java:57-87).  The Vector API leaves the
  * order of reduceLanes unspecified; a pairwise tree is used here. */
-static float dot_vector(const float *a, const float *b, int n, int lane) {
+static inline float dot_vector(const float *a, const float *b, int n, int lane) {
   float acc[4][16];
   memset(acc, 0, sizeof(acc));
   int upper = n - n % lane;
@@ -125,8 +125,13 @@ static float dot_vector(const float *a, const float *b, int n, int lane) {
   return sum;
 }
 
+/* The lane counts of AVX2 and AVX-512 hosts as constants, so the compiler can vectorize the
+ * lane loops (the arithmetic and its order are those of dot_vector). */
 static float dot(const float *a, const float *b, int n, int mode) {
-  return mode == 0 ? dot_scalar(a, b, n) : dot_vector(a, b, n, mode);
+  if (mode == 0) return dot_scalar(a, b, n);
+  if (mode == 16) return dot_vector(a, b, n, 16);
+  if (mode == 8) return dot_vector(a, b, n, 8);
+  return dot_vector(a, b, n, mode);
 }
 
 /* axpy: dst += alpha*src.  Scalar: separate mul and add; vector: FMA body, scalar tail. */

@@ -122,6 +122,20 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
 
 
+def build_native(out_path: str) -> str:
+    """Compile the same oracle.c for this host (-O3 -march=native) to ``out_path``: the
+    benchmark's CPU baseline, built on the machine it is timed on."""
+    subprocess.run(["make", "-s", "-C", _HERE, "native", f"NATIVE_OUT={out_path}"], check=True)
+    return out_path
+
+
+def set_library(path: str) -> None:
+    """Use the oracle library at ``path`` (e.g. a build_native() build) for every later call."""
+    global _lib, _LIB_PATH
+    _LIB_PATH = path
+    _lib = None
+
+
 def lib():
     global _lib
     if _lib is None:
