@@ -766,8 +766,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
   // least 64 queries of each head (measured: Gemma3 d = 256 prefill 13% faster with 2 heads
   // than with 4, Gemma 4 d = 512 3% faster with 1 than with 4, Qwen3-4B shape 4% faster with 2
   // than with 4).
-  const int hpw_tile =
-      largest_pow2_divisor_upto(rep, std::max(1, prefill_waves(d.head_dim) / 4));
+  const int hpw_tile = largest_pow2_divisor_upto(rep, prefill_max_heads(d.head_dim));
   const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, hpw_tile);
   if (!row_kernel_supports(d.head_dim, hpw_row))
     return fail(ctx, NVA_E_UNSUPPORTED, "head_dim %d has no row kernel in this build",

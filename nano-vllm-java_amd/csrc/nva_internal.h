@@ -176,11 +176,12 @@ constexpr int kPrefillTablePages = 128;
 // Most pages one row-kernel work item may span (its block ids are staged in LDS).
 constexpr int kRowTablePages = 64;
 
-// Waves per prefill workgroup at this head dim; each wave owns 16 queries of one head.
+// Waves per prefill workgroup at this head dim (each wave owns 16 queries of one head; at
+// d = 512 a pair of waves shares them, one half of the head dims each).
 int prefill_waves(int head_dim);
+// Most query heads one prefill workgroup carries at this head dim.
+int prefill_max_heads(int head_dim);
 // Query rows per prefill workgroup for a given heads-per-workgroup choice.
-inline int prefill_tile_queries(int head_dim, int heads_per_wg) {
-  return 16 * (prefill_waves(head_dim) / heads_per_wg);
-}
+int prefill_tile_queries(int head_dim, int heads_per_wg);
 
 }  // namespace nva

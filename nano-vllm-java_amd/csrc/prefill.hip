@@ -365,6 +365,228 @@ prefill_kernel(TileLaunch a) {
   }  // segments
 }
 
+// Head dim 512 (Gemma 4 global layers) with the head split over a wave pair: one 8-wave
+// workgroup per CU, waves w and w + 4 own the same 16 queries and the dims [256 h, 256 h + 256)
+// of half h = w / 4.  Each wave forms the partial S^T of its half (64 MFMAs per 16-key tile),
+// the pair adds the two partials through LDS in a fixed order (S = S_0 + S_1 in both waves, so
+// both hold the same scores and run the same softmax) and each accumulates O^T for its own
+// 256 dims.  Q and O take 64 registers each instead of 128, so two waves fit per SIMD and
+// one covers the other's LDS waits (one 256-dim wave per SIMD left the matrix pipe idle for
+// every LDS read).  Every wave executes the exchange barrier of every tile, active or not.
+template <int HPW>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+prefill512_kernel(TileLaunch a) {
+  constexpr int D = 512, DH = 256, KT = 16, NW = 8;
+  constexpr int DQ = DH / 4;         // QK steps per lane group: dims DH*half + DQ*g + [0, DQ)
+  constexpr int NB = DH / 16;        // O^T blocks of the half: block 4*hh+bb, dims 64*hh+4r+bb
+  constexpr int H64 = DH / 64;
+  constexpr int C4 = D / 4;          // 16-byte chunks per K/V row
+  constexpr int NI = KT * C4 / 64;   // load instructions per tensor per tile
+  constexpr int LPW = NI / NW;
+  constexpr int TILE = KT * D;
+  static_assert(HPW == 1, "one query head per workgroup");
+  static_assert(LPW >= 1 && NI % NW == 0, "tile does not split evenly over the waves");
+  __shared__ __attribute__((aligned(16))) float sk0[TILE];
+  __shared__ __attribute__((aligned(16))) float sv0[TILE];
+  __shared__ __attribute__((aligned(16))) float sk1[TILE];
+  __shared__ __attribute__((aligned(16))) float sv1[TILE];
+  __shared__ f32x4 spart[NW][64];  // each wave's partial S^T of the current tile
+  __shared__ int32_t stab[kTablePages];
+
+  const int slot = blockIdx.x;
+  const int seg_end = a.seg_off[slot + 1];
+  for (int seg = a.seg_off[slot]; seg < seg_end; seg++) {
+  __syncthreads();
+  const TileItem it = a.items[seg];
+  const int rep = a.hq / a.hkv;
+  const int kvh = blockIdx.y / rep;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = blockIdx.y;  // one head per workgroup: grid y runs over the query heads
+  const int half = wave >> 2;
+  const int qb = wave & 3;
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15;
+  const int g = lane >> 4;
+  const int W = a.window;
+  const int off = it.klen - it.qlen;
+  const float sl2 = a.scale * kLog2e;
+
+  const int qi = it.q0 + qb * 16 + i;
+  const bool qvalid = qi < it.qlen;
+  const int qic = qvalid ? qi : it.qlen - 1;
+  const int aq = off + qic;
+  const int vis_lo = W > 0 ? max(0, aq - W + 1) : 0;
+  const int vis_hi = aq + 1;
+  const int wq0 = it.q0 + qb * 16;
+  const bool wave_active = wq0 < it.qlen;
+  const int wq1 = min(wq0 + 15, it.qlen - 1);
+  const int wlo_min = W > 0 ? max(0, off + wq0 - W + 1) : 0;
+  const int wlo_max = W > 0 ? max(0, off + wq1 - W + 1) : 0;
+  const int whi_min = off + wq0 + 1;
+  const int whi_max = off + wq1 + 1;
+
+  float qr[DQ];
+  {
+    const float *qp = a.q + ((size_t)(it.qstart + qic) * a.hq + h) * D + DH * half + DQ * g;
+#pragma unroll
+    for (int s = 0; s < DQ; s += 4) {
+      const float4 x = ld4(qp + s);
+      qr[s] = x.x;
+      qr[s + 1] = x.y;
+      qr[s + 2] = x.z;
+      qr[s + 3] = x.w;
+    }
+  }
+  f32x4 o[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) o[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  const size_t rs = (size_t)a.hkv * D;
+  const float *kbase = a.kv.k + (size_t)kvh * D;
+  const float *vbase = a.kv.v + (size_t)kvh * D;
+  int blk0 = 0;
+  if (a.kv.paged) {
+    const int bs = a.kv.block_size;
+    blk0 = it.ks / bs;
+    const int npages = (it.ke - 1) / bs - blk0 + 1;
+    const int32_t *table = a.kv.table + (size_t)it.seq * a.kv.bt_stride + blk0;
+    for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[j];
+    __syncthreads();
+  }
+  auto issue_tile = [&](int kt, float *dk, float *dv) {
+#pragma unroll
+    for (int p = 0; p < LPW; p++) {
+      const int gi = p * NW + wave;
+      const int q = gi * 64 + lane;
+      const int r = q / C4;
+      const int pos = q - r * C4;
+      const int key = min(kt + r, it.ke - 1);
+      const int64_t row = tile_row(a.kv, stab, blk0, it.kbase, key);
+      const float *gk = kbase + row * rs + kswz<D>(pos, r) * 4;
+      const float *gv = vbase + row * rs + pos * 4;
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)gk,
+          (__attribute__((address_space(3))) void *)(dk + gi * 256), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)gv,
+          (__attribute__((address_space(3))) void *)(dv + gi * 256), 16, 0, 0);
+    }
+  };
+
+  auto compute_tile = [&](int kt, const float *sk, const float *sv) {
+    const bool active = wave_active && kt < whi_max && kt + KT > wlo_min;
+    f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (active) {
+      // Partial S^T over this half: A[key][k] = K[i][DH*half + DQ*g + s], chunk
+      // 64*half + 16*g + s/4 of row i, at kswz(chunk, i).
+      const float *kr = sk + i * D;
+#pragma unroll
+      for (int s = 0; s < DQ; s += 4) {
+        const float4 kk = ld4(kr + 4 * kswz<D>(64 * half + 16 * g + (s >> 2), i));
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qr[s], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qr[s + 1], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[s + 2], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[s + 3], st, 0, 0, 0);
+      }
+      spart[wave][lane] = st;
+    }
+    __syncthreads();
+    if (!active) return;
+    const f32x4 other = spart[wave ^ 4][lane];
+    st = half == 0 ? st + other : other + st;  // S_0 + S_1 in both waves of the pair
+    const bool full = (kt + KT <= whi_min) && (kt >= wlo_max);
+
+    // p[v] holds key kt + 4*g + v for query i (log2-scaled).
+    float p[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float x = st[v] * sl2;
+      if (!full) {
+        const int key = kt + 4 * g + v;
+        x = (key >= vis_lo && key < vis_hi) ? x : -INFINITY;
+      }
+      p[v] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = max4_lanes(mx);
+    const bool need = mx > m_run + kLazyRescale;
+    if (__any(need)) {
+      const float mn = need ? mx : m_run;
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mn);
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < NB; b++) o[b] *= alpha;
+      m_run = mn;
+    }
+    const float ms = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      p[v] = __builtin_amdgcn_exp2f(p[v] - ms);
+      l_run += p[v];
+    }
+
+    // O^T += V^T P^T over this half's dims: step s contracts key 4*g + s (= p[s] in this lane).
+    const float *vrow = sv + 4 * g * D + DH * half + 4 * i;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const float *vp = vrow + s * D;
+#pragma unroll
+      for (int hh = 0; hh < H64; hh++) {
+        const float4 vv = ld4(vp + 64 * hh);
+        o[4 * hh + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[s], o[4 * hh + 0], 0, 0, 0);
+        o[4 * hh + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[s], o[4 * hh + 1], 0, 0, 0);
+        o[4 * hh + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[s], o[4 * hh + 2], 0, 0, 0);
+        o[4 * hh + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[s], o[4 * hh + 3], 0, 0, 0);
+      }
+    }
+  };
+
+  const int ntiles = (it.ke - it.ks + KT - 1) / KT;
+  issue_tile(it.ks, sk0, sv0);
+  for (int t = 0; t < ntiles; t += 2) {
+    const int kt = it.ks + t * KT;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 1 < ntiles) issue_tile(kt + KT, sk1, sv1);
+    compute_tile(kt, sk0, sv0);
+    if (t + 1 >= ntiles) break;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t + 2 < ntiles) issue_tile(kt + 2 * KT, sk0, sv0);
+    compute_tile(kt + KT, sk1, sv1);
+  }
+
+  const float l_tot = sum4_lanes(l_run);
+  if (!qvalid || !wave_active) continue;
+  float *op;
+  float inv = 1.0f;
+  const bool partial = it.part >= 0;
+  size_t pidx = 0;
+  if (!partial) {
+    inv = l_tot == 0.0f ? 0.0f : 1.0f / l_tot;
+    op = a.out + ((size_t)(it.qstart + qi) * a.hq + h) * D + DH * half;
+  } else {
+    pidx = ((size_t)it.part + (size_t)(qi - it.q0) * it.nsplit + it.split) * a.hq + h;
+    op = a.part_acc + pidx * D + DH * half;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int r = 4 * g + v;
+#pragma unroll
+    for (int hh = 0; hh < H64; hh++)
+      st4(op + 64 * hh + 4 * r, make_float4(o[4 * hh][v] * inv, o[4 * hh + 1][v] * inv,
+                                          o[4 * hh + 2][v] * inv, o[4 * hh + 3][v] * inv));
+  }
+  if (partial && g == 0 && half == 0) {
+    a.part_m[pidx] = m_run;
+    a.part_l[pidx] = l_tot;
+  }
+  }  // segments
+}
+
 namespace {
 
 // Keys per tile and waves per workgroup for head dim D.
@@ -374,7 +596,7 @@ constexpr int key_tile() {
 }
 template <int D>
 constexpr int tile_waves() {
-  return D == 512 ? 4 : 8;
+  return 8;
 }
 
 template <int D>
@@ -410,10 +632,21 @@ int prefill_waves(int head_dim) {
   return tile_waves<128>();
 }
 
+// At d = 512 a wave pair shares 16 queries (prefill512_kernel), one query head per workgroup;
+// otherwise each wave owns 16 queries and up to a quarter of the waves share a head group.
+int prefill_max_heads(int head_dim) {
+  return head_dim == 512 ? 1 : std::max(1, prefill_waves(head_dim) / 4);
+}
+
+int prefill_tile_queries(int head_dim, int heads_per_wg) {
+  const int query_blocks = head_dim == 512 ? prefill_waves(head_dim) / 2 : prefill_waves(head_dim);
+  return 16 * (query_blocks / heads_per_wg);
+}
+
 bool prefill_kernel_supports(int head_dim, int heads_per_wg) {
   return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) &&
          (heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 || heads_per_wg == 8) &&
-         heads_per_wg <= prefill_waves(head_dim);
+         heads_per_wg <= prefill_max_heads(head_dim);
 }
 
 namespace {
@@ -447,7 +680,14 @@ int blocks_per_cu_d(int hpw) {
 int prefill_blocks_per_cu(int head_dim, int heads_per_wg) {
   if (head_dim == 64) return blocks_per_cu_d<64>(heads_per_wg);
   if (head_dim == 256) return blocks_per_cu_d<256>(heads_per_wg);
-  if (head_dim == 512) return blocks_per_cu_d<512>(heads_per_wg);
+  if (head_dim == 512) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, prefill512_kernel<1>, 512, 0) !=
+            hipSuccess ||
+        b < 1)
+      b = 1;
+    return b;
+  }
   return blocks_per_cu_d<128>(heads_per_wg);
 }
 
@@ -457,7 +697,10 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int hpw, hipStream_t s) {
     case 64: return launch_prefill_d<64>(a, hpw, s);
     case 128: return launch_prefill_d<128>(a, hpw, s);
     case 256: return launch_prefill_d<256>(a, hpw, s);
-    case 512: return launch_prefill_d<512>(a, hpw, s);
+    case 512:
+      if (hpw != 1) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((prefill512_kernel<1>), dim3(a.num_slots, a.hq), dim3(512), 0, s, a);
+      return hipGetLastError();
     default: return hipErrorInvalidValue;
   }
 }
