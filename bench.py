@@ -273,7 +273,14 @@ def time_o_proj(ctx, attn_out, wl, steps, warmup, hidden=1024, seed=21):
     flops = 2.0 * m * hidden * k
     byts = 4.0 * (m * k + hidden * k + m * hidden)
     tf = flops / (ms * 1e-3) / 1e12
-    return {"kernel": "linear_kernel (fp32 MFMA 32x32x2; K slices from a per-CU cost model, reduce kernel when sliced; gemv_kernel at <= 8 rows)",
+    blocks = ((hidden + 31) // 32) * ((m + 31) // 32)
+    if m <= 8:
+        kern = "gemv_kernel (weight-streaming GEMV, <= 8 rows)"
+    elif blocks <= torch.cuda.get_device_properties(x.device).multi_processor_count:
+        kern = "skinny_kernel<8,2> (fp32 MFMA 32x32x2, one 32x32 block per workgroup, K over 8 waves)"
+    else:
+        kern = "linear_kernel (fp32 MFMA 32x32x2, 128x128 tiles; K slices from a per-CU cost model)"
+    return {"kernel": kern,
             "shape": f"[{m}, {k}] x [{hidden}, {k}]^T", "ms": round(ms, 5),
             "tflops": round(tf, 2), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
             "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}

@@ -1719,6 +1719,36 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
     tm.done();
     return NVA_OK;
   }
+  const int cus = std::max(1, ctx->num_cus);
+  const int64_t blocks = (int64_t)((out + 31) / 32) * ((rows + 31) / 32);
+  if (blocks <= cus) {
+    // Decode batches: 32 x 32 blocks (one workgroup per CU, its LDS ring fills the CU), K
+    // sliced only while the blocks leave CUs idle: the most slices s with blocks * s <= CUs
+    // that keep a 32-k stage for every wave of a slice.
+    const int kmin = linear_skinny_waves() * 32;
+    int splits = 1;
+    while (blocks * (splits + 1) <= cus && in / (splits + 1) >= kmin) splits++;
+    const int kps = ((in + splits - 1) / splits + 31) / 32 * 32;
+    LinearLaunch g{};
+    g.x = x;
+    g.w = weight;
+    g.bias = bias;
+    g.y = y;
+    g.m = rows;
+    g.n = out;
+    g.k = in;
+    g.splits = (in + kps - 1) / kps;
+    g.k_per_split = kps;
+    if (g.splits > 1) {
+      HIP_TRY(ctx, ctx->d_lin.reserve((size_t)g.splits * rows * out * sizeof(float)),
+              "linear partial buffer");
+      g.part = static_cast<float *>(ctx->d_lin.ptr);
+    }
+    Timed tm(ctx, "linear");
+    HIP_TRY(ctx, launch_skinny(g, ctx->stream), "skinny linear kernel launch");
+    tm.done();
+    return NVA_OK;
+  }
   // K slices: the count s that minimises a per-CU cost model.  A CU runs the K tiles of its
   // workgroups at about the same rate whether one or two are resident, so the kernel takes
   // ceil(tiles * s / CUs) workgroup rounds of ceil(K tiles / s) K tiles each (about 2.1 us per
@@ -1728,7 +1758,6 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
                         ((rows + linear_tile_rows() - 1) / linear_tile_rows());
   const int bk = linear_k_tile();
   const int nkt = (in + bk - 1) / bk;
-  const int cus = std::max(1, ctx->num_cus);
   int splits = 1;
   double best = 0.0;
   for (int sl = 1; sl <= std::max(1, nkt / 4); sl++) {

@@ -6,9 +6,15 @@
 // output in its gemv panel order; here the sum runs over MFMA steps and split-K slices, so the
 // result agrees to fp32 rounding (checked against the oracle within the attention tolerance).
 //
-// Mapping onto CDNA4.  A workgroup owns a 128 x 128 tile of y and one K slice: four waves of
-// 64 x 64 (2 x 2 blocks of v_mfma_f32_32x32x2_f32), or, when the grid has no more workgroups
-// than CUs, eight waves of 32 x 64, so each SIMD still has two waves to switch between.
+// Mapping onto CDNA4.  Three kernels by shape:
+//   * gemv_kernel for at most 8 rows (a weight-streaming GEMV, below);
+//   * skinny_kernel when the 32 x 32 blocks of y number at most one per CU (decode batches of
+//     tens to a few hundred rows): one block per workgroup, K split over its eight waves, each
+//     streaming its own K range through a private LDS ring (below);
+//   * linear_kernel otherwise.  A workgroup owns a 128 x 128 tile of y and one K slice: four
+//     waves of 64 x 64 (2 x 2 blocks of v_mfma_f32_32x32x2_f32), or, when the grid has no more
+//     workgroups than CUs, eight waves of 32 x 64, so each SIMD still has two waves to switch
+//     between.
 //   * x and W are both K-contiguous, so the A operand (x rows) and the B operand (W rows) are
 //     read the same way: for each 8-wide K chunk a lane (i, h) reads one float4 of its row
 //     (elements 4h .. 4h + 3), which feeds 4 MFMA steps -- step s contracts k = 4h + s, a
@@ -19,8 +25,8 @@
 //     cycles were conflict stalls).
 //   * Output block layout (32 x 32, 16 values per lane): value r of lane (i, h) is row
 //     8 * (r / 4) + 4 * h + r % 4, column i -- lanes 0..31 write 128 contiguous bytes.
-//   * When the tile grid alone cannot fill the chip (decode: a few rows), K is split over
-//     blockIdx.z; slices write partial sums and linear_reduce_kernel adds them in slice order,
+//   * When the grid alone cannot fill the chip, K is split over blockIdx.z (both MFMA
+//     kernels); slices write partial sums and linear_reduce_kernel adds them in slice order,
 //     plus the bias.  (Letting the last slice of a tile reduce in place needs a device-scope
 //     release per slice, which on this multi-XCD part writes back L2 and cost more than the
 //     separate launch.)
@@ -34,8 +40,27 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int kSkinnyWaves = 8;  // waves of a skinny_kernel workgroup (two per SIMD)
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// ds_read_b128 the compiler does not see as an LDS read, so it adds no wait for every
+// outstanding LDS copy before it (it cannot tell a ring's stages apart); the caller waits
+// (lgkmcnt) before using the value, tying the wait to the registers.
+__device__ __forceinline__ f4v lds_read4(const float *p) {
+  const unsigned addr = (unsigned)(size_t)(const __attribute__((address_space(3))) float *)p;
+  f4v v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Wait until at most N vector memory operations are outstanding.
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 }  // namespace
 
@@ -202,6 +227,133 @@ __global__ void __launch_bounds__(256) linear_reduce_kernel(LinearLaunch a) {
   }
 }
 
+// Tens to a few hundred rows (decode batches): one 32 x 32 block of y per workgroup, so the
+// 256-row, 1024-column o_proj alone has 256 workgroups, and the K slice split over the
+// workgroup's NW waves.  No operand is shared between the waves, so each wave streams its own
+// K range through a private ring of PF LDS stages (32 x rows and 32 W rows of 32 k each),
+// copied with global_load_lds_dwordx4 so that every copy instruction reads whole 128-byte
+// rows, with the chunk swizzle of the tiled kernel; no barrier until the end.  A stage is read
+// into registers whole, its refill issued, then its 16 MFMAs run: lane (i, h) holds
+// k = kt + 16h .. kt + 16h + 15 of row i as four float4, and MFMA step j contracts
+// k = kt + 16h + j (the same permutation for A and B).  The waves' blocks meet in LDS and are
+// added in wave order (plus the bias, or into the slice's partial plane).  Eight waves with two
+// stages each (128 KB of LDS, one workgroup per CU) measured faster than four waves with four
+// (one wave per SIMD), and than staging through registers instead of LDS.
+template <int NW, int PF>
+__global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
+  constexpr int KI = 32;       // k per stage
+  constexpr int ST = 32 * KI;  // floats per operand per stage
+  __shared__ __attribute__((aligned(16))) float ring[NW][PF][2][ST];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+  const int kb = blockIdx.z * a.k_per_split;
+  const int ke = min(a.k, kb + a.k_per_split);
+  const int per = (ke - kb + NW * KI - 1) / (NW * KI) * KI;
+  const int wk0 = kb + w * per, wk1 = min(ke, wk0 + per);
+  const int iters = wk1 > wk0 ? (wk1 - wk0 + KI - 1) / KI : 0;
+
+  // Copy instruction g moves rows [8g, 8g + 8) of a stage: lane l takes row 8g + l / 8, LDS
+  // chunk position l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7).  Rows and columns past
+  // the edge copy the last valid row (their sums are not stored); chunks past the wave's K
+  // range copy a valid address and are zeroed at use.
+  const int lrow = lane >> 3, lpos = lane & 7;
+  auto issue = [&](int it, int st) {
+    const int kt = wk0 + it * KI;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int r = 8 * g + lrow;
+      int kc = kt + 4 * (lpos ^ ((r >> 1) & 7));
+      kc = kc < wk1 ? kc : 0;
+      const int xr = min(m0 + r, a.m - 1);
+      const int wr = min(n0 + r, a.n - 1);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)(a.x + (size_t)xr * a.k + kc),
+          (__attribute__((address_space(3))) void *)(&ring[w][st][0][g * 8 * KI]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void *)(a.w + (size_t)wr * a.k + kc),
+          (__attribute__((address_space(3))) void *)(&ring[w][st][1][g * 8 * KI]), 16, 0, 0);
+    }
+  };
+  constexpr int OPS = 8;  // copy instructions per stage
+  f32x16 acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    acc0[r] = 0.0f;
+    acc1[r] = 0.0f;
+  }
+#pragma unroll
+  for (int p = 0; p < PF; p++)
+    if (p < iters) issue(p, p);
+  for (int it = 0; it < iters; it += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+      if (it + p < iters) {
+        // Stage p landed: every later stage issued so far (OPS operations each) may still be in
+        // flight.
+        if (it + p + PF - 1 < iters)
+          wait_vm<OPS * (PF - 1)>();
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const int kt = wk0 + (it + p) * KI;
+        const float *sa = ring[w][p][0], *sb = ring[w][p][1];
+        const int sw = i * KI, sx = (i >> 1) & 7;
+        // The whole stage goes to registers first, so its refill is issued before the MFMAs.
+        f4v av[4], bv[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          av[q] = lds_read4(sa + sw + 4 * ((4 * h + q) ^ sx));
+          bv[q] = lds_read4(sb + sw + 4 * ((4 * h + q) ^ sx));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]),
+                       "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3])::"memory");
+        if (it + p + PF < iters) issue(it + p + PF, p);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          if (kt + 4 * (4 * h + q) >= wk1) {
+            av[q] = f4v{0.f, 0.f, 0.f, 0.f};
+            bv[q] = f4v{0.f, 0.f, 0.f, 0.f};
+          }
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][0], bv[q][0], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][1], bv[q][1], acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][2], bv[q][2], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][3], bv[q][3], acc1, 0, 0, 0);
+        }
+      }
+    }
+  }
+  // The wave's block goes to its own first stage (its copies have all landed and been read).
+  // Value r of lane (i, h): row 8 * (r / 4) + 4 * h + r % 4, column i.
+  float *red = ring[w][0][0];
+#pragma unroll
+  for (int r = 0; r < 16; r++) red[(8 * (r >> 2) + 4 * h + (r & 3)) * 32 + i] = acc0[r] + acc1[r];
+  __syncthreads();
+  const bool direct = a.splits == 1;
+  float *dst = direct ? a.y : a.part + (size_t)blockIdx.z * a.m * a.n;
+  for (int u = threadIdx.x; u < 256; u += 64 * NW) {
+    const int row = u >> 3, c = 4 * (u & 7);
+    float4 s = ld4(&ring[0][0][0][row * 32 + c]);
+#pragma unroll
+    for (int v = 1; v < NW; v++) {
+      const float4 t = ld4(&ring[v][0][0][row * 32 + c]);
+      s.x += t.x;
+      s.y += t.y;
+      s.z += t.z;
+      s.w += t.w;
+    }
+    if (m0 + row >= a.m) continue;
+    float *yr = dst + (size_t)(m0 + row) * a.n;
+    const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int col = n0 + c + e;
+      if (col < a.n) yr[col] = direct && a.bias ? sv[e] + a.bias[col] : sv[e];
+    }
+  }
+}
+
 // Few rows (decode batches): y = x W^T + bias as a weight-streaming GEMV.  Wave w of
 // workgroup b owns output columns n0 = (4b + w) * CPW .. n0 + CPW - 1 for all M rows: lane l
 // reads the 16-byte chunks l, l + 64, ... of those W rows (non-temporal loads: W is read once)
@@ -304,6 +456,17 @@ hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+namespace {
+
+hipError_t launch_reduce(const LinearLaunch &a, hipStream_t s) {
+  const size_t units = (a.n & 3) == 0 ? (size_t)a.m * a.n / 4 : (size_t)a.m * a.n;
+  const unsigned blocks = (unsigned)std::min<size_t>((units + 255) / 256, 8192);
+  hipLaunchKernelGGL(linear_reduce_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_linear(const LinearLaunch &a, hipStream_t s) {
   if (a.m <= 0 || a.n <= 0) return hipSuccess;
   const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM, a.splits);
@@ -313,14 +476,21 @@ hipError_t launch_linear(const LinearLaunch &a, hipStream_t s) {
     hipLaunchKernelGGL(linear_kernel<2>, grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
-  const size_t units = (a.n & 3) == 0 ? (size_t)a.m * a.n / 4 : (size_t)a.m * a.n;
-  const unsigned blocks = (unsigned)std::min<size_t>((units + 255) / 256, 8192);
-  hipLaunchKernelGGL(linear_reduce_kernel, dim3(blocks), dim3(256), 0, s, a);
-  return hipGetLastError();
+  return launch_reduce(a, s);
+}
+
+hipError_t launch_skinny(const LinearLaunch &a, hipStream_t s) {
+  if (a.m <= 0 || a.n <= 0) return hipSuccess;
+  const dim3 grid((a.n + 31) / 32, (a.m + 31) / 32, a.splits);
+  hipLaunchKernelGGL((skinny_kernel<kSkinnyWaves, 2>), grid, dim3(64 * kSkinnyWaves), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  return launch_reduce(a, s);
 }
 
 int linear_tile_rows() { return BM; }
 int linear_tile_cols() { return BN; }
 int linear_k_tile() { return BK; }
+int linear_skinny_waves() { return kSkinnyWaves; }
 
 }  // namespace nva

@@ -154,6 +154,10 @@ hipError_t launch_zero(float *out, size_t n, hipStream_t s);
 hipError_t launch_linear(const LinearLaunch &a, hipStream_t s);
 // Weight-streaming GEMV for at most linear_gemv_max_rows() rows (no split, no partials).
 hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s);
+// 32 x 32 blocks of y, one per workgroup, K split over the workgroup's linear_skinny_waves()
+// waves; runs the reduce when splits > 1.
+hipError_t launch_skinny(const LinearLaunch &a, hipStream_t s);
+int linear_skinny_waves();
 int linear_gemv_max_rows();
 int linear_tile_rows();
 int linear_tile_cols();
