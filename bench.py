@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--flush", action="store_true",
                     help="write 512 MB between steps so K/V that fits the 256 MB Infinity Cache "
                          "is read from HBM (kernel timings exclude the flush)")
+    ap.add_argument("--linear-vs-vendor", action="store_true",
+                    help="time o_proj (nva_linear_forward) and torch.addmm (hipBLASLt) on the "
+                         "decode and prefill o_proj shapes, one JSON line per shape")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy three times (the "
                          "known-size reference for the FETCH_SIZE/WRITE_SIZE counters)")
@@ -284,6 +287,44 @@ def time_o_proj(ctx, attn_out, wl, steps, warmup, hidden=1024, seed=21):
             "shape": f"[{m}, {k}] x [{hidden}, {k}]^T", "ms": round(ms, 5),
             "tflops": round(tf, 2), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
             "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}
+
+
+# o_proj shapes of Qwen3-0.6B (hidden 1024, Hq * d = 2048): decode batches and the 4096-token
+# prefill step.
+LINEAR_SHAPES = [(64, 2048, 1024), (128, 2048, 1024), (256, 2048, 1024), (4096, 2048, 1024)]
+
+
+def linear_vs_vendor(args, ctx):
+    """nva_linear_forward against torch.addmm (hipBLASLt) on the same fp32 operands, both timed
+    with HIP events over `steps` back-to-back calls after `warmup`; max-abs error of each
+    against a float64 product."""
+    import torch
+    from nanollvm_amd import Linear
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    for m, k, n in LINEAR_SHAPES:
+        x = torch.randn((m, k), device="cuda", generator=g)
+        w = torch.randn((n, k), device="cuda", generator=g) / math.sqrt(k)
+        bias = torch.zeros(n, device="cuda")
+        lin = Linear(w)
+        ref = x.double() @ w.double().T
+        wt = w.T
+        res = {}
+        for name, fn in (("nva", lambda: lin.forward(x, ctx)), ("hipblaslt", lambda: torch.addmm(bias, x, wt))):
+            y = fn()
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / args.steps
+            res[name] = {"us": round(ms * 1e3, 2), "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
+                         "max_abs_vs_f64": float((y.double() - ref).abs().max())}
+        print(json.dumps({"shape": f"[{m}, {k}] x [{n}, {k}]^T", **res}), flush=True)
 
 
 def kernel_a_roofline(wl, stats):
@@ -571,6 +612,10 @@ def main():
 
     torch.cuda.init()
     ctx = Context(0)
+    if args.linear_vs_vendor:
+        linear_vs_vendor(args, ctx)
+        ctx.close()
+        return
     if args.workload:
         line = bench_extra(args, ctx)
         ctx.close()
