@@ -64,6 +64,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
 def copy_calibration():
+    """Kernels of known HBM traffic for scaling FETCH_SIZE / WRITE_SIZE: a device-to-device copy
+    (reads and writes COPY_BYTES) and a read-only sum (reads COPY_BYTES, writes 4 bytes)."""
     import torch
     src = torch.ones(COPY_BYTES // 4, device="cuda")
     dst = torch.empty_like(src)
@@ -71,7 +73,13 @@ def copy_calibration():
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"copy calibration: 3 x {COPY_BYTES} bytes device-to-device")
+    del dst
+    total = None
+    for _ in range(3):
+        total = src.sum()
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 x {COPY_BYTES} bytes device-to-device, 3 x {COPY_BYTES} bytes "
+        f"read by a sum ({float(total):.0f})")
 
 
 def measured_traffic(kernel):

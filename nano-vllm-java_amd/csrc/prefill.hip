@@ -83,15 +83,17 @@ __device__ __forceinline__ float sum4_lanes(float x) {
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 
 // LDS position of chunk c of K row r (and, being an involution, the chunk at position c):
-// the low three bits are XORed with r & 7; from d = 256 on, where a lane group's chunks span a
-// whole 256-byte bank period, bit 3 is also XORed with the parity of the chunk's lane group.
-// Measured with SQ_LDS_BANK_CONFLICT: zero conflicts for d = 128, 256 and 512 (r & 15 alone:
-// 33% of the LDS-active cycles at d = 128).
+// the low three bits are XORed with r & 7; from d = 256 on, where a lane group's 16 or more
+// chunks span a whole 256-byte bank period, bit 3 is also XORed with bit 4 of the chunk, which
+// tells adjacent lane groups apart (a lane group reads chunks 16g + j at d = 256 and, in the
+// half-row waves of d = 512, 64 half + 16g + j).  Measured with SQ_LDS_BANK_CONFLICT: zero
+// conflicts for d = 128, 256 and 512 (r & 15 alone: 33% of the LDS-active cycles at d = 128;
+// at d = 512, bit 3 from the parity of c / 32: 30%).
 template <int D>
 __device__ __forceinline__ int kswz(int c, int r) {
-  constexpr int GS = D / 16;  // chunks per lane group
+  constexpr int GS = D / 16;  // chunks per lane group of a full-row read
   int x = r & 7;
-  if constexpr (GS >= 16) x |= ((c / GS) & 1) << 3;
+  if constexpr (GS >= 16) x |= ((c >> 4) & 1) << 3;
   return c ^ x;
 }
 
