@@ -671,6 +671,18 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     merges.push_back({r.qrow, parts, n, 0});
     parts += n;
   }
+  // Items within at most two pages carry the pages' block ids (RowItem::blk_a / blk_b).
+  if (key.paged) {
+    const int bs = key.block_size;
+    for (RowItem &it : items) {
+      if (it.kend <= it.kbeg) continue;
+      const int p0 = it.kbeg / bs, p1 = (it.kend - 1) / bs;
+      if (p1 - p0 > 1) continue;
+      const int32_t *t = ctx->tables.data() + (size_t)it.seq * ctx->bt_stride;
+      it.blk_a = t[p0] + 1;
+      it.blk_b = p1 > p0 ? t[p1] : 0;
+    }
+  }
   // Longest items first: the workgroups dispatched last are the short row tails, so the chip
   // drains quickly at the end of the launch.  Items carry their own partial slot, so the
   // order does not change any result.

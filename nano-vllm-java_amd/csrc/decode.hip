@@ -119,9 +119,12 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   // Stage the item's block ids in LDS once (the host caps items at kRowTablePages pages), so
   // a row address waits on an LDS read instead of on every K/V load issued before it.
   int blk0 = 0;
-  if (a.kv.paged) {
+  // An item within at most two pages carries their block ids, so its first K/V loads wait on no
+  // table read (small steps: 12.6 -> 11.7 us for the 8-row Qwen3 decode after a flush).
+  const bool inl = a.kv.paged && it.blk_a != 0;
+  if (a.kv.paged) blk0 = page_of(a.kv, it.kbeg);
+  if (a.kv.paged && !inl) {
     const int32_t *table = a.kv.table + (size_t)it.seq * a.kv.bt_stride;
-    blk0 = page_of(a.kv, it.kbeg);
     const int npages = it.kend > it.kbeg ? page_of(a.kv, it.kend - 1) - blk0 + 1 : 0;
     for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[blk0 + j];
     __syncthreads();
@@ -148,7 +151,15 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     for (int u = 0; u < UH; u++) {
       const int t = g0 + u * TPW + sub;
       ok[u] = t < it.kend;
-      const int64_t row = kv_row(a.kv, stab, blk0, it.kbase, ok[u] ? t : it.kbeg);
+      const int tt = ok[u] ? t : it.kbeg;
+      int64_t row;
+      if (inl) {
+        const int blk = page_of(a.kv, tt);
+        const int id = blk == blk0 ? it.blk_a - 1 : it.blk_b;
+        row = (int64_t)id * a.kv.block_size + (tt - blk * a.kv.block_size);
+      } else {
+        row = kv_row(a.kv, stab, blk0, it.kbase, tt);
+      }
 #pragma unroll
       for (int j = 0; j < VPL; j++) {
         kr[u][j] = ld4_stream(kp + row * rs + LPT * 4 * j);

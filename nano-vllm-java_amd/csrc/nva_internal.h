@@ -19,7 +19,9 @@ struct RowItem {
   int32_t kbeg;   // first key (absolute position in the sequence)
   int32_t kend;   // one past the last key
   int32_t part;   // partial-result slot, or -1
-  int32_t pad0, pad1;
+  // Paged items within at most two pages: block id of the first page + 1 (0: the kernel stages
+  // the item's block ids from the table instead) and of the second page.
+  int32_t blk_a, blk_b;
 };
 
 // Combines the partials of one split row (nparts >= 2) or zero-fills a row with no visible
