@@ -196,7 +196,46 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
     ms = (t1 - t0) * 1e3 / steps
     log(f"{label}: {ms:.4f} ms/step; kernels " + ", ".join(
         f"{n}={s[1] / max(s[0], 1):.4f}ms x{s[0]}" for n, s in stats.items() if s[0]))
-    return ms, stats, time_step_plan(ctx, wl, step)
+    gms = graph_step_ms(ctx, step, steps, flush)
+    if gms is not None:
+        log(f"{label}: {gms:.4f} ms/step replaying the step as a HIP graph")
+    plan = time_step_plan(ctx, wl, step)
+    plan["graph_ms_per_step"] = None if gms is None else round(gms, 5)
+    return ms, stats, plan
+
+
+def graph_step_ms(ctx, step, steps, flush=None):
+    """The same layer step captured once into a HIP graph (torch.cuda.graph on a side stream the
+    context is switched to) and replayed `steps` times: wall time per replay, or None when the
+    capture fails.  The plan and every buffer already exist from the eager steps, so the
+    captured calls launch kernels only."""
+    import torch
+    s = torch.cuda.Stream()
+    ctx.set_stream(s)
+    try:
+        with torch.cuda.stream(s):
+            step()
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                step()
+            s.synchronize()
+            g.replay()
+            s.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):  # back to back, like the eager steps
+                if flush is not None:
+                    flush()
+                g.replay()
+            s.synchronize()
+            total = time.perf_counter() - t0
+        return total * 1e3 / steps
+    except RuntimeError as e:
+        log(f"graph capture failed: {e}")
+        return None
+    finally:
+        torch.cuda.synchronize()
+        ctx.set_stream()
 
 
 def time_step_prepare(ctx, wl, reps=30):
@@ -236,7 +275,7 @@ def step_metadata(ctx, wl, plan):
     plan (build, upload); the sum is what a scheduler step pays once, before the kernels of its
     first layer."""
     out = time_step_prepare(ctx, wl)
-    out.update(plan)
+    out.update({k: v for k, v in plan.items() if k != "graph_ms_per_step"})
     out["per_step_host_us"] = round(out["build_upload_us"] + plan["plans_per_step"] *
                                     (plan["plan_build_us"] + plan["plan_upload_us"]), 1)
     return out
@@ -388,6 +427,7 @@ def bench_decode(args, ctx):
                      "algorithmic_bytes_per_launch": byts},
         "kernel_a": kernel_a_roofline(wl, stats),
         "step_metadata": step_metadata(ctx, wl, plan),
+        "graph_ms_per_step": plan["graph_ms_per_step"],
     }
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
@@ -435,6 +475,7 @@ def bench_prefill(args, ctx):
                      "algorithmic_flops_per_launch": flops},
         "kernel_a": kernel_a_roofline(wl, stats),
         "step_metadata": step_metadata(ctx, wl, plan),
+        "graph_ms_per_step": plan["graph_ms_per_step"],
     }
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
@@ -519,6 +560,7 @@ def bench_extra(args, ctx):
     line["lower_bound_ms"] = round(bound, 5)
     line["step_metadata"] = step_metadata(ctx, wl, plan)
     line["attention_ms"] = round(kms.get("attention", 0.0), 5)
+    line["graph_ms_per_step"] = plan["graph_ms_per_step"]
     rope.close()
     arena.close()
     return line
@@ -664,6 +706,7 @@ def main():
             "roofline": dec["roofline"],
             "kernel_a": dec["kernel_a"],
             "step_metadata": dec["step_metadata"],
+            "graph_ms_per_step": dec["graph_ms_per_step"],
             "o_proj": dec["o_proj"],
         })
     else:

@@ -113,6 +113,14 @@ class Context:
     def handle(self):
         return self._h
 
+    def set_stream(self, stream: Optional[torch.cuda.Stream] = None) -> None:
+        """Run the context's work on ``stream`` (default: torch's current stream), e.g. the
+        stream a HIP graph is being captured on."""
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        _check(self._h, N.load().nva_ctx_set_stream(self._h, ctypes.c_void_p(s.cuda_stream)),
+               "set_stream")
+        self._stream = s
+
     # ---- Context.java API
     def bind_kv_cache(self, arena: "KvCacheArena") -> None:
         self._kv = arena
