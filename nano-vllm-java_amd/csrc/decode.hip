@@ -18,8 +18,8 @@
 //     (VPL = 2 at D = 512): each wave load instruction fetches TPW = 64/LPT whole rows, i.e.
 //     contiguous 128-byte lines, and all HPW query heads of the KV head reuse the registers
 //     (K/V are read from HBM exactly once per KV head);
-//   * the dot products are reduced across the LPT lanes with DPP row ops and one swizzle (no
-//     LDS traffic); each group of LPT lanes is an independent online-softmax stream;
+//   * the dot products are reduced across the LPT lanes with DPP row ops and gfx950's row
+//     swaps (no LDS traffic); each group of LPT lanes is an independent online-softmax stream;
 //   * the 4*TPW streams of the workgroup are merged through LDS at the end, and either the
 //     output row (unsplit item) or the partial (m, l, acc) of the chunk is written.
 // HBM bytes per work item: chunk * 2 * D * 4 per KV head (+ q, + the partial or output row).
@@ -45,9 +45,19 @@ __device__ __forceinline__ float dpp(float x) {
   return __builtin_amdgcn_update_dpp(0.0f, x, CTRL, 0xF, 0xF, false);
 }
 
-__device__ __forceinline__ float swizzle_xor16(float x) {
-  // Bit-mode swizzle within 32-lane halves: and_mask 0x1F, or_mask 0, xor_mask 0x10.
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+// x[lane] + x[lane ^ 16] (resp. lane ^ 32) in every lane, by gfx950's row-swap instructions:
+// the swap of x with itself leaves one of the two values in each output, and the sum of the
+// two is the same bits in both lanes of a pair.  No LDS round trip, unlike ds_swizzle or
+// ds_bpermute.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Sum of x over aligned groups of LPT lanes; every lane of the group receives the sum.
@@ -57,8 +67,8 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (LPT >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
   if constexpr (LPT >= 8) x += dpp<0x141>(x);  // row_half_mirror
   if constexpr (LPT >= 16) x += dpp<0x140>(x); // row_mirror
-  if constexpr (LPT >= 32) x += swizzle_xor16(x);
-  if constexpr (LPT >= 64) x += __shfl_xor(x, 32);
+  if constexpr (LPT >= 32) x = add_xor16(x);
+  if constexpr (LPT >= 64) x = add_xor32(x);
   return x;
 }
 
