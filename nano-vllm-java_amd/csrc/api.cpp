@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -241,6 +242,10 @@ struct nva_ctx {
   DevBuf d_k_rot;    // fused path scratch for rotated k
   DevBuf d_v_norm;   // fused path scratch for normalised v (dense prefill with a v norm)
   DevBuf d_lin;      // split-K partial sums of the linear kernel
+  // o_proj backend (NVA_LINEAR_BACKEND at context creation): auto = GEMV up to a few rows,
+  // hipBLASLt above; native = this library's kernels only; vendor = hipBLASLt for every shape.
+  enum LinearBackend { kLinearAuto, kLinearNative, kLinearVendor } linear_backend = kLinearAuto;
+  VendorGemm *gemm = nullptr;  // created on the first hipBLASLt call
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
 
   // This device's address of the no-allocation scratch array (null if the lookup failed).
@@ -1113,6 +1118,10 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
   }
   ctx->stream = ctx->own_stream;
   ctx->scratch = scratch_address(device, &ctx->scratch_err);
+  if (const char *b = getenv("NVA_LINEAR_BACKEND")) {
+    if (!strcmp(b, "native")) ctx->linear_backend = nva_ctx::kLinearNative;
+    if (!strcmp(b, "vendor")) ctx->linear_backend = nva_ctx::kLinearVendor;
+  }
   *out = ctx;
   return NVA_OK;
 }
@@ -1136,6 +1145,7 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   ctx->d_k_rot.release();
   ctx->d_v_norm.release();
   ctx->d_lin.release();
+  vendor_gemm_destroy(ctx->gemm);
   ctx->d_gather.release();
   (void)hipEventDestroy(ctx->fork_ev);
   (void)hipEventDestroy(ctx->join_ev);
@@ -1714,6 +1724,27 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
     return fail(ctx, NVA_E_UNSUPPORTED, "linear needs in %% 4 == 0 (got %d)", in);
   if (!aligned16(x) || !aligned16(weight))
     return fail(ctx, NVA_E_ARG, "x and weight must be 16-byte aligned device pointers");
+  const int cus = std::max(1, ctx->num_cus);
+  const int64_t blocks = (int64_t)((out + 31) / 32) * ((rows + 31) / 32);
+  // auto: the library's GEMV and 32 x 32-block kernels while the output fits one block per CU
+  // (decode batches: they beat hipBLASLt's kernel plus its per-call host cost), hipBLASLt for
+  // larger GEMMs, where its stream-K tiles beat the library's 128 x 128 tiles.
+  const bool vendor = ctx->linear_backend == nva_ctx::kLinearVendor ||
+                      (ctx->linear_backend == nva_ctx::kLinearAuto &&
+                       rows > linear_gemv_max_rows() && blocks > cus);
+  if (vendor) {
+    // A plain GEMM: hipBLASLt's fp32 kernels with the bias in their epilogue (vendor_gemm.cpp).
+    std::string e;
+    if (!ctx->gemm) {
+      ctx->gemm = vendor_gemm_create(ctx->device, &e);
+      if (!ctx->gemm) return fail(ctx, NVA_E_HIP, "%s", e.c_str());
+    }
+    Timed tm(ctx, "linear");
+    if (!vendor_gemm_run(ctx->gemm, x, weight, bias, y, rows, in, out, ctx->stream, &e))
+      return fail(ctx, NVA_E_HIP, "%s", e.c_str());
+    tm.done();
+    return NVA_OK;
+  }
   if (rows <= linear_gemv_max_rows()) {
     // A few rows: stream W once (GEMV), no tiles, no K slices.
     LinearLaunch g{};
@@ -1731,8 +1762,6 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
     tm.done();
     return NVA_OK;
   }
-  const int cus = std::max(1, ctx->num_cus);
-  const int64_t blocks = (int64_t)((out + 31) / 32) * ((rows + 31) / 32);
   if (blocks <= cus) {
     // Decode batches: 32 x 32 blocks (one workgroup per CU, its LDS ring fills the CU), K
     // sliced only while the blocks leave CUs idle: the most slices s with blocks * s <= CUs

@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <string>
 #include <stdint.h>
 
 #include <algorithm>
@@ -159,6 +161,14 @@ hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s);
 // 32 x 32 blocks of y, one per workgroup, K split over the workgroup's linear_skinny_waves()
 // waves; runs the reduce when splits > 1.
 hipError_t launch_skinny(const LinearLaunch &a, hipStream_t s);
+
+// hipBLASLt for o_proj batches (vendor_gemm.cpp): one per context, created on first use.
+struct VendorGemm;
+VendorGemm *vendor_gemm_create(int device, std::string *err);
+void vendor_gemm_destroy(VendorGemm *v);
+// y[rows, out] = x[rows, in] w[out, in]^T (+ bias[out]) on stream; false with *err set on failure.
+bool vendor_gemm_run(VendorGemm *v, const float *x, const float *w, const float *bias, float *y,
+                     int rows, int in, int out, hipStream_t stream, std::string *err);
 int linear_skinny_waves();
 int linear_gemv_max_rows();
 int linear_tile_rows();

@@ -409,8 +409,10 @@ class RMSNorm:
 
 class Linear:
     """Linear.Row(weight [out, in], bias) (layers/Linear.java:296-335): ``forward(x, ctx)`` is
-    Ops.linear, y = x W^T + b, on fp32 MFMA.  ``weight``/``bias`` are float32 device tensors
-    kept resident, as the model's weights are."""
+    Ops.linear, y = x W^T + b, in fp32: the library's GEMV and block kernels for decode batches,
+    hipBLASLt for larger GEMMs (the context's NVA_LINEAR_BACKEND, read at creation, can force
+    either).  ``weight``/``bias`` are
+    float32 device tensors kept resident, as the model's weights are."""
 
     def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
         if weight.dim() != 2:

@@ -1,7 +1,13 @@
 """o_proj (Linear.Row -> Ops.linear) on fp32 MFMA through the C ABI, against the oracle's
 restatement of the reference's gemv at decode shapes, and against float64 at the full prefill
-shapes.  Bar: max-abs 1e-4 and rel-L2 1e-5, the path's floating-point tolerance."""
+shapes.  Bar: max-abs 1e-4 and rel-L2 1e-5, the path's floating-point tolerance.
 
+Every case runs on each o_proj backend a context can be created with (NVA_LINEAR_BACKEND):
+auto (the library's GEMV and 32 x 32-block kernels for decode batches, hipBLASLt for larger
+GEMMs), native (the library's GEMV, 32 x 32-block and 128 x 128-tile kernels for every shape)
+and vendor (hipBLASLt for every shape)."""
+
+import os
 import sys
 
 import numpy as np
@@ -23,9 +29,18 @@ def say(msg):
     sys.stdout.flush()
 
 
-@pytest.fixture(scope="module")
-def ctx():
-    c = Context(0)
+@pytest.fixture(scope="module", params=["auto", "native", "vendor"])
+def ctx(request):
+    old = os.environ.get("NVA_LINEAR_BACKEND")
+    os.environ["NVA_LINEAR_BACKEND"] = request.param  # read when the context is created
+    try:
+        c = Context(0)
+    finally:
+        if old is None:
+            del os.environ["NVA_LINEAR_BACKEND"]
+        else:
+            os.environ["NVA_LINEAR_BACKEND"] = old
+    say(f"o_proj backend {request.param}")
     yield c
     c.close()
 
