@@ -14,14 +14,18 @@
 //   * one workgroup (4 waves) per (work item, KV head, group of HPW query heads); a work item
 //     is one query row and a chunk of its key range (the host splits long rows so that every
 //     workgroup reads about the same number of bytes and the grid has thousands of groups);
-//   * a K/V row (D fp32) is read by LPT = min(64, D/4) lanes, VPL = D/(4*LPT) float4 each
-//     (VPL = 2 at D = 512): each wave load instruction fetches TPW = 64/LPT whole rows, i.e.
-//     contiguous 128-byte lines, and all HPW query heads of the KV head reuse the registers
+//   * a K/V row (D fp32) is read by LPT lanes, VPL float4 each (VPL = 2 from d = 32 on, with at
+//     most 4 heads per workgroup): each wave load instruction fetches TPW = 64/LPT whole rows,
+//     i.e. contiguous 128-byte lines, and all HPW query heads of the KV head reuse the registers
 //     (K/V are read from HBM exactly once per KV head);
+//   * paged K/V with power-of-two pages: a wave's rows of one register group lie in one page,
+//     so their address is formed in scalar registers and the loads take a fixed per-lane offset
+//     (the vector ALU does the attention arithmetic only);
 //   * the dot products are reduced across the LPT lanes with DPP row ops and gfx950's row
 //     swaps (no LDS traffic); each group of LPT lanes is an independent online-softmax stream;
-//   * the 4*TPW streams of the workgroup are merged through LDS at the end, and either the
-//     output row (unsplit item) or the partial (m, l, acc) of the chunk is written.
+//   * the TPW streams of a wave fold together with lane shuffles, the 4 waves' results merge
+//     through LDS, and either the output row (unsplit item) or the partial (m, l, acc) of the
+//     chunk is written.
 // HBM bytes per work item: chunk * 2 * D * 4 per KV head (+ q, + the partial or output row).
 #include "nva_internal.h"
 
@@ -88,17 +92,35 @@ __device__ __forceinline__ int64_t kv_row(const KvView &kv, const int32_t *stab,
 
 }  // namespace
 
+// Lane layout of the K/V rows, per head dim and heads per workgroup: a row is read by LPT lanes
+// holding VPL float4 each, so a lane's part of a dot product is 4 * VPL fmas before the LPT-lane
+// reduction; TPW rows per wave load instruction, UH rows per lane per register group and
+// G = TPW * UH rows per wave per group.  VPL = 2 from d = 32 on halves the reduction steps per
+// key against one float4 per lane (d = 128: 16 lanes per row, all within one DPP row); eight
+// heads per workgroup keep one float4 per lane, as q and the accumulators then take 16
+// registers per head.
 template <int D, int HPW>
+struct RowShape {
+  static constexpr int VPL = D >= 512 ? 2 : (D >= 32 && HPW <= 4 ? 2 : 1);
+  static constexpr int LPT = D / (4 * VPL);
+  static constexpr int TPW = 64 / LPT;
+  static constexpr int UH = 4 / VPL;
+  static constexpr int G = TPW * UH;
+};
+
+// PAGED_ALIGNED: paged K/V whose block size is a power of two and a multiple of G.  A wave's
+// register groups then start at multiples of G, so each group's G rows lie in one page and
+// are consecutive there: the group's first row address is formed once in scalar registers
+// (block id from the staged table, read only when the page changes) and every lane adds a
+// fixed 32-bit offset, so a K/V load costs no vector instruction.  Other layouts (dense K/V,
+// small pages) form each lane's row address from its key.
+template <int D, int HPW, bool PAGED_ALIGNED>
 __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
-  constexpr int LPT = D / 4 < 64 ? D / 4 : 64;  // lanes per K/V row
-  constexpr int VPL = D / (4 * LPT);            // float4 per lane per row
-  constexpr int TPW = 64 / LPT;                 // rows per wave load instruction
-  constexpr int UH = 4 / VPL > 0 ? 4 / VPL : 1;  // rows per stream per register group
-  constexpr int G = TPW * UH;                    // rows per wave per register group
-  constexpr int NS = 4 * TPW;                   // softmax streams per workgroup
-  __shared__ float sm_m[NS][HPW];
-  __shared__ float sm_l[NS][HPW];
-  __shared__ float4 sm_acc[NS][HPW][LPT * VPL];
+  using S = RowShape<D, HPW>;
+  constexpr int LPT = S::LPT, VPL = S::VPL, TPW = S::TPW, UH = S::UH, G = S::G;
+  __shared__ float sm_m[4][HPW];
+  __shared__ float sm_l[4][HPW];
+  __shared__ float4 sm_acc[4][HPW][D / 4];
   __shared__ int32_t stab[kRowTablePages];  // block ids of the pages this item touches
 
   const int rep = a.hq / a.hkv;
@@ -110,27 +132,28 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   const int kvh = gy / groups;
   const int h0 = kvh * rep + (gy - kvh * groups) * HPW;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane / LPT;
   const int c = lane - sub * LPT;
 
   // Lane c holds dims [4c + 4*LPT*j, +4) for j < VPL, so each load instruction is contiguous.
+  // q is pre-scaled by scale * log2(e): the dot products come out in log2 units.
+  const float sl2 = a.scale * 1.4426950408889634f;
   float4 qv[HPW][VPL];
 #pragma unroll
   for (int h = 0; h < HPW; h++)
 #pragma unroll
-    for (int j = 0; j < VPL; j++)
-      qv[h][j] = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + (c + LPT * j) * 4);
-  const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+    for (int j = 0; j < VPL; j++) {
+      const float4 x = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + (c + LPT * j) * 4);
+      qv[h][j] = make_float4(x.x * sl2, x.y * sl2, x.z * sl2, x.w * sl2);
+    }
 
   const size_t rs = (size_t)a.hkv * D;
-  const float *kp = a.kv.k + (size_t)kvh * D + c * 4;
-  const float *vp = a.kv.v + (size_t)kvh * D + c * 4;
   // Stage the item's block ids in LDS once (the host caps items at kRowTablePages pages), so
   // a row address waits on an LDS read instead of on every K/V load issued before it.
   int blk0 = 0;
   // An item within at most two pages carries their block ids, so its first K/V loads wait on no
-  // table read (small steps: 12.6 -> 11.7 us for the 8-row Qwen3 decode after a flush).
+  // table read.
   const bool inl = a.kv.paged && it.blk_a != 0;
   if (a.kv.paged) blk0 = page_of(a.kv, it.kbeg);
   if (a.kv.paged && !inl) {
@@ -150,30 +173,81 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     for (int j = 0; j < VPL; j++) acc[h][j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
+  // Aligned layouts start the groups at the multiple of G at or below the first key; the keys
+  // before it are masked.
+  const int gfirst = PAGED_ALIGNED ? (it.kbeg & ~(G - 1)) : it.kbeg;
+  const uint32_t lane_off = (uint32_t)(sub * rs + c * 4);  // floats from the group's first row
+  const float *kbase_h = a.kv.k + (size_t)kvh * D;
+  const float *vbase_h = a.kv.v + (size_t)kvh * D;
+  int cur_page = -1;      // page whose first row is cur_row0 (wave-uniform)
+  int64_t cur_row0 = 0;
+
   // Two register groups of UH rows per stream: the loads of the next group are issued before
   // the current one is folded, so every wave keeps loads in flight while it computes.  The
-  // issue is unconditional (keys past the end load the item's first row and are masked), which
-  // keeps the wait before each fold to exactly the current group's loads.
+  // issue is unconditional (a group past the end reloads the item's first group, masked),
+  // which keeps the wait before each fold to exactly the current group's loads.
   float4 kra[UH][VPL], vra[UH][VPL], krb[UH][VPL], vrb[UH][VPL];
   bool oka[UH], okb[UH];
   auto issue = [&](int g0, float4(&kr)[UH][VPL], float4(&vr)[UH][VPL], bool(&ok)[UH]) {
+    if constexpr (PAGED_ALIGNED) {
+      const int gq = g0 < it.kend ? g0 : gfirst;
+      const int p = gq >> a.kv.bs_shift;
+      if (p != cur_page) {
+        const int id = inl ? (p == blk0 ? it.blk_a - 1 : it.blk_b)
+                           : __builtin_amdgcn_readfirstlane(stab[p - blk0]);
+        cur_page = p;
+        cur_row0 = (int64_t)id * a.kv.block_size - ((int64_t)p << a.kv.bs_shift);
+      }
+      const int64_t row = cur_row0 + gq;
+      const float *kb = kbase_h + row * rs;
+      const float *vb = vbase_h + row * rs;
+      // Lane offsets (floats) of the group's rows.  In a partial group (the item's first or
+      // last, or one past its end that reloads the first) masked keys may sit on page slots
+      // never written (any bits, NaN included), so each lane reads the group's key nearest its
+      // own inside [kbeg, kend) instead, whose finite V row adds exactly 0 at weight 0.
+      uint32_t off[UH];
+      if (g0 >= it.kbeg && g0 + G <= it.kend) {
 #pragma unroll
-    for (int u = 0; u < UH; u++) {
-      const int t = g0 + u * TPW + sub;
-      ok[u] = t < it.kend;
-      const int tt = ok[u] ? t : it.kbeg;
-      int64_t row;
-      if (inl) {
-        const int blk = page_of(a.kv, tt);
-        const int id = blk == blk0 ? it.blk_a - 1 : it.blk_b;
-        row = (int64_t)id * a.kv.block_size + (tt - blk * a.kv.block_size);
+        for (int u = 0; u < UH; u++) {
+          ok[u] = true;
+          off[u] = lane_off + (uint32_t)(u * TPW * rs);
+        }
       } else {
-        row = kv_row(a.kv, stab, blk0, it.kbase, tt);
+#pragma unroll
+        for (int u = 0; u < UH; u++) {
+          const int t = g0 + u * TPW + sub;
+          ok[u] = t >= it.kbeg && t < it.kend;
+          const int tq = gq + u * TPW + sub;
+          const int tc = min(max(tq, it.kbeg), it.kend - 1);
+          off[u] = (uint32_t)__mul24(tc - gq, (int)rs) + c * 4;
+        }
       }
 #pragma unroll
-      for (int j = 0; j < VPL; j++) {
-        kr[u][j] = ld4_stream(kp + row * rs + LPT * 4 * j);
-        vr[u][j] = ld4_stream(vp + row * rs + LPT * 4 * j);
+      for (int u = 0; u < UH; u++)
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+          kr[u][j] = ld4_stream(kb + off[u] + LPT * 4 * j);
+          vr[u][j] = ld4_stream(vb + off[u] + LPT * 4 * j);
+        }
+    } else {
+#pragma unroll
+      for (int u = 0; u < UH; u++) {
+        const int t = g0 + u * TPW + sub;
+        ok[u] = t < it.kend;
+        const int tt = ok[u] ? t : it.kbeg;
+        int64_t row;
+        if (inl) {
+          const int blk = page_of(a.kv, tt);
+          const int id = blk == blk0 ? it.blk_a - 1 : it.blk_b;
+          row = (int64_t)id * a.kv.block_size + (tt - blk * a.kv.block_size);
+        } else {
+          row = kv_row(a.kv, stab, blk0, it.kbase, tt);
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+          kr[u][j] = ld4_stream(kbase_h + row * rs + c * 4 + LPT * 4 * j);
+          vr[u][j] = ld4_stream(vbase_h + row * rs + c * 4 + LPT * 4 * j);
+        }
       }
     }
   };
@@ -199,7 +273,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       float mx = -INFINITY;
 #pragma unroll
       for (int u = 0; u < UH; u++) {
-        s[u] = ok[u] ? s[u] * sl2 : -INFINITY;
+        s[u] = ok[u] ? s[u] : -INFINITY;
         mx = fmaxf(mx, s[u]);
       }
       const float mn = fmaxf(m[h], mx);
@@ -233,7 +307,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     }
   };
 
-  int g0 = it.kbeg + wave * G;
+  int g0 = gfirst + wave * G;
   if (g0 < it.kend) {
     issue(g0, kra, vra, oka);
     for (;;) {
@@ -248,28 +322,55 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     }
   }
 
-  const int stream = wave * TPW + sub;
+  // The TPW streams of a wave fold into the lanes of stream 0 (each lane with the stream
+  // LPT * 2^i lanes above it, lower stream first), then the waves' streams merge through LDS.
 #pragma unroll
-  for (int h = 0; h < HPW; h++) {
-    if (c == 0) {
-      sm_m[stream][h] = m[h];
-      sm_l[stream][h] = l[h];
+  for (int dist = LPT; dist < 64; dist <<= 1) {
+#pragma unroll
+    for (int h = 0; h < HPW; h++) {
+      const float mo = __shfl_xor(m[h], dist);
+      const float lo = __shfl_xor(l[h], dist);
+      const float M = fmaxf(m[h], mo);
+      const float Ms = M == -INFINITY ? 0.0f : M;
+      const float ea = __builtin_amdgcn_exp2f(m[h] - Ms);
+      const float eb = __builtin_amdgcn_exp2f(mo - Ms);
+      l[h] = fmaf(lo, eb, l[h] * ea);
+#pragma unroll
+      for (int j = 0; j < VPL; j++) {
+        float4 &x = acc[h][j];
+        x.x = fmaf(__shfl_xor(x.x, dist), eb, x.x * ea);
+        x.y = fmaf(__shfl_xor(x.y, dist), eb, x.y * ea);
+        x.z = fmaf(__shfl_xor(x.z, dist), eb, x.z * ea);
+        x.w = fmaf(__shfl_xor(x.w, dist), eb, x.w * ea);
+      }
+      m[h] = M;
     }
+  }
+  if (sub == 0) {
 #pragma unroll
-    for (int j = 0; j < VPL; j++) sm_acc[stream][h][c + LPT * j] = acc[h][j];
+    for (int h = 0; h < HPW; h++) {
+      if (c == 0) {
+        sm_m[wave][h] = m[h];
+        sm_l[wave][h] = l[h];
+      }
+#pragma unroll
+      for (int j = 0; j < VPL; j++) sm_acc[wave][h][c + LPT * j] = acc[h][j];
+    }
   }
   __syncthreads();
 
   // sm_acc[.][h][cc] holds dims [4cc, 4cc + 4) of head h.
-  for (int idx = threadIdx.x; idx < HPW * LPT * VPL; idx += blockDim.x) {
-    const int h = idx / (LPT * VPL);
-    const int cc = idx - h * (LPT * VPL);
+  for (int idx = threadIdx.x; idx < HPW * (D / 4); idx += blockDim.x) {
+    const int h = idx / (D / 4);
+    const int cc = idx - h * (D / 4);
     float M = -INFINITY;
-    for (int s = 0; s < NS; s++) M = fmaxf(M, sm_m[s][h]);
+#pragma unroll
+    for (int s = 0; s < 4; s++) M = fmaxf(M, sm_m[s][h]);
     const float Ms = M == -INFINITY ? 0.0f : M;
     float L = 0.0f;
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < NS; s++) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
       const float e = __builtin_amdgcn_exp2f(sm_m[s][h] - Ms);
       L = fmaf(sm_l[s][h], e, L);
       const float4 x = sm_acc[s][h][cc];
@@ -406,16 +507,25 @@ __global__ void __launch_bounds__(NW * 64) merge_kernel(MergeLaunch a) {
 
 namespace {
 
+template <int D, int HPW>
+void launch_row_dh(const RowLaunch &a, const dim3 &grid, hipStream_t s) {
+  constexpr int G = RowShape<D, HPW>::G;
+  if (a.kv.paged && a.kv.bs_shift >= 0 && a.kv.block_size % G == 0)
+    hipLaunchKernelGGL((row_attention_kernel<D, HPW, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((row_attention_kernel<D, HPW, false>), grid, dim3(256), 0, s, a);
+}
+
 template <int D>
 hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
   const dim3 grid(a.num_items * (a.hkv * ((a.hq / a.hkv) / hpw)));
   switch (hpw) {
-    case 1: hipLaunchKernelGGL((row_attention_kernel<D, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((row_attention_kernel<D, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((row_attention_kernel<D, 4>), grid, dim3(256), 0, s, a); break;
+    case 1: launch_row_dh<D, 1>(a, grid, s); break;
+    case 2: launch_row_dh<D, 2>(a, grid, s); break;
+    case 4: launch_row_dh<D, 4>(a, grid, s); break;
     case 8:
       if constexpr (D <= 256) {
-        hipLaunchKernelGGL((row_attention_kernel<D, 8>), grid, dim3(256), 0, s, a);
+        launch_row_dh<D, 8>(a, grid, s);
         break;
       }
       return hipErrorInvalidValue;
