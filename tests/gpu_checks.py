@@ -7,11 +7,12 @@ import numpy as np
 import torch
 
 from cases import rel_l2
-from nanollvm_amd import Attention, KvCacheArena
+from nanollvm_amd import Attention, KvCacheArena, RMSNorm, RotaryEmbedding
 from oracle import oracle as O
 
 MAX_ABS = 1e-4
 REL_L2 = 1e-5
+EPS = 1e-6
 
 
 def say(msg):
@@ -105,3 +106,64 @@ def fill_normal(arena, seed, layer=0):
         for s in range(0, flat.numel(), 1 << 28):
             flat[s:s + (1 << 28)].normal_(generator=g)
     torch.cuda.synchronize()
+
+
+def _norm_heads(x, w, one_plus):
+    return O.rms_norm(x.reshape(-1, x.shape[-1]), w, EPS, one_plus).reshape(x.shape)
+
+
+def check_fused(ctx, case, name, q_w, k_w, one_plus=False, v_norm=False, max_pos=None,
+                theta=1e4, outputs=True, norms=True):
+    """The per-head norms + RoPE + Attention.forward chain through nva_norm_rope_attention_forward
+    against the oracle chain (normHeads, RoPE, Attention.forward): rotated q/k (when `outputs`)
+    and every page byte bit-exact, attention within the bar.  norms=False passes no q/k norm at
+    all (RoPE only); outputs=False passes no q_out/k_out."""
+    wl = case.wl
+    say(f"{name}: tokens={wl.tokens} hq={wl.hq} hkv={wl.hkv} d={wl.d} W={wl.window} "
+        f"bs={wl.block_size} one_plus={one_plus} v_norm={v_norm} outputs={outputs}")
+    max_pos = max_pos or 512
+    table = O.rope_table(wl.d, max_pos, theta)
+    rope = RotaryEmbedding(ctx, wl.d, wl.d, max_pos, theta, cos_sin=table)
+    if case.paged:
+        arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+        arena.write(0, 0, case.k_cache)
+        arena.write(0, 1, case.v_cache)
+    else:
+        arena = KvCacheArena(ctx, 1, 2, 16, wl.hkv, wl.d)
+    try:
+        ctx.set(**wl.meta.context_args())
+        ctx.bind_kv_cache(arena)
+        attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
+        qn = RMSNorm(None if q_w is None else dev(q_w), EPS, one_plus) if norms else None
+        kn = RMSNorm(None if k_w is None else dev(k_w), EPS, one_plus) if norms else None
+        vn = RMSNorm.weightless(EPS) if v_norm else None
+        q_out = torch.empty(case.q.shape, dtype=torch.float32, device="cuda") if outputs else None
+        k_out = torch.empty(case.k.shape, dtype=torch.float32, device="cuda") if outputs else None
+        out = attn.forward_with_norm_rope(rope, wl.meta.positions, dev(case.q), dev(case.k),
+                                          dev(case.v), ctx, q_norm=qn, k_norm=kn, v_norm=vn,
+                                          q_out=q_out, k_out=k_out)
+        # Oracle chain: normHeads(q), normHeads(k) [, vNorm(v)], RoPE, Attention.forward.
+        nq = _norm_heads(case.q, q_w, one_plus) if norms else case.q
+        nk = _norm_heads(case.k, k_w, one_plus) if norms else case.k
+        qr, kr = O.rope_forward(table, wl.meta.positions, nq, nk)
+        torch.cuda.synchronize()
+        if outputs:
+            assert np.array_equal(bits(q_out.cpu().numpy()), bits(qr)), "q not bit-exact"
+            assert np.array_equal(bits(k_out.cpu().numpy()), bits(kr)), "k not bit-exact"
+        case.q, case.k = qr, kr
+        if v_norm:
+            case.v = _norm_heads(case.v, None, False)
+        want, kc, vc = case.oracle(threads=8)
+        got = out.cpu().numpy()
+        err = float(np.max(np.abs(got - want))) if got.size else 0.0
+        rl2 = rel_l2(got, want)
+        say(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+        assert np.all(np.isfinite(got))
+        assert err <= MAX_ABS and rl2 <= REL_L2, (err, rl2)
+        if case.paged:
+            assert np.array_equal(bits(arena.get_key_cache(0)), bits(kc)), "K pages differ"
+            assert np.array_equal(bits(arena.get_value_cache(0)), bits(vc)), "V pages differ"
+    finally:
+        ctx.clear()
+        arena.close()
+        rope.close()

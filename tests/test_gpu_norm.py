@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from cases import Case, rel_l2, small_cases
+from gpu_checks import EPS, check_fused
 from nanollvm_amd import Attention, Context, KvCacheArena, RMSNorm, RotaryEmbedding
 from nanollvm_amd import workloads as W
 from oracle import oracle as O
@@ -19,7 +20,6 @@ pytestmark = pytest.mark.gpu
 
 MAX_ABS = 1e-4
 REL_L2 = 1e-5
-EPS = 1e-6
 
 
 def say(msg):
@@ -65,62 +65,6 @@ def test_rms_norm_order_known_answer(ctx):
     got = RMSNorm.weightless(0.0).forward(dev(x), ctx).cpu().numpy()
     inv = np.float32(1.0 / np.sqrt(2.0 ** 17))
     assert got[0, 1] == inv and got[0, 0] == np.float32(np.float32(4096.0) * inv)
-
-
-def _norm_heads(x, w, one_plus):
-    return O.rms_norm(x.reshape(-1, x.shape[-1]), w, EPS, one_plus).reshape(x.shape)
-
-
-def check_fused(ctx, case, name, q_w, k_w, one_plus=False, v_norm=False, max_pos=None,
-                theta=1e4):
-    wl = case.wl
-    say(f"{name}: tokens={wl.tokens} hq={wl.hq} hkv={wl.hkv} d={wl.d} W={wl.window} "
-        f"one_plus={one_plus} v_norm={v_norm}")
-    max_pos = max_pos or 512
-    table = O.rope_table(wl.d, max_pos, theta)
-    rope = RotaryEmbedding(ctx, wl.d, wl.d, max_pos, theta, cos_sin=table)
-    if case.paged:
-        arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
-        arena.write(0, 0, case.k_cache)
-        arena.write(0, 1, case.v_cache)
-    else:
-        arena = KvCacheArena(ctx, 1, 2, 16, wl.hkv, wl.d)
-    try:
-        ctx.set(**wl.meta.context_args())
-        ctx.bind_kv_cache(arena)
-        attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
-        qn = RMSNorm(None if q_w is None else dev(q_w), EPS, one_plus)
-        kn = RMSNorm(None if k_w is None else dev(k_w), EPS, one_plus)
-        vn = RMSNorm.weightless(EPS) if v_norm else None
-        q_out = torch.empty(case.q.shape, dtype=torch.float32, device="cuda")
-        k_out = torch.empty(case.k.shape, dtype=torch.float32, device="cuda")
-        out = attn.forward_with_norm_rope(rope, wl.meta.positions, dev(case.q), dev(case.k),
-                                          dev(case.v), ctx, q_norm=qn, k_norm=kn, v_norm=vn,
-                                          q_out=q_out, k_out=k_out)
-        # Oracle chain: normHeads(q), normHeads(k) [, vNorm(v)], RoPE, Attention.forward.
-        nq = _norm_heads(case.q, q_w, one_plus)
-        nk = _norm_heads(case.k, k_w, one_plus)
-        qr, kr = O.rope_forward(table, wl.meta.positions, nq, nk)
-        torch.cuda.synchronize()
-        assert np.array_equal(bits(q_out.cpu().numpy()), bits(qr)), "q not bit-exact"
-        assert np.array_equal(bits(k_out.cpu().numpy()), bits(kr)), "k not bit-exact"
-        case.q, case.k = qr, kr
-        if v_norm:
-            case.v = _norm_heads(case.v, None, False)
-        want, kc, vc = case.oracle(threads=8)
-        got = out.cpu().numpy()
-        err = float(np.max(np.abs(got - want))) if got.size else 0.0
-        rl2 = rel_l2(got, want)
-        say(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e}")
-        assert np.all(np.isfinite(got))
-        assert err <= MAX_ABS and rl2 <= REL_L2, (err, rl2)
-        if case.paged:
-            assert np.array_equal(bits(arena.get_key_cache(0)), bits(kc)), "K pages differ"
-            assert np.array_equal(bits(arena.get_value_cache(0)), bits(vc)), "V pages differ"
-    finally:
-        ctx.clear()
-        arena.close()
-        rope.close()
 
 
 SMALL = small_cases()
