@@ -217,8 +217,9 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
         for (int u = 0; u < UH; u++) {
           const int t = g0 + u * TPW + sub;
           ok[u] = t >= it.kbeg && t < it.kend;
+          // (A group past the end reads only the item's first key: its loads are never folded.)
           const int tq = gq + u * TPW + sub;
-          const int tc = min(max(tq, it.kbeg), it.kend - 1);
+          const int tc = g0 >= it.kend ? it.kbeg : min(max(tq, it.kbeg), it.kend - 1);
           off[u] = (uint32_t)__mul24(tc - gq, (int)rs) + c * 4;
         }
       }
@@ -394,30 +395,46 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   }
 }
 
-// Row-wide merge for plans whose split rows have few partials (prefill segments): one workgroup
-// per row covers all heads, each thread folding the partials of one float4 of one head in order.
+// Row-wide merge for plans whose split rows have at most kMergeRowsMaxParts partials (prefill
+// segments): one workgroup per row covers all heads, each thread folding the partials of one
+// float4 of one head in order.  All of a thread's partial loads are issued before the first is
+// used, so the merge costs one memory round trip instead of two per partial.
+constexpr int kMergeRowsMaxParts = 4;
 __global__ void __launch_bounds__(256) merge_rows_kernel(MergeLaunch a) {
   const MergeItem it = a.items[blockIdx.x];
   const int d4 = a.head_dim >> 2;
+  const int n = it.nparts;  // 0 .. kMergeRowsMaxParts
   for (int idx = threadIdx.x; idx < a.hq * d4; idx += blockDim.x) {
     const int h = idx / d4;
     const int cc = idx - h * d4;
     float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (it.nparts > 0) {
+    if (n > 0) {
+      float pm[kMergeRowsMaxParts], pl[kMergeRowsMaxParts];
+      float4 px[kMergeRowsMaxParts];
+#pragma unroll
+      for (int p = 0; p < kMergeRowsMaxParts; p++) {
+        const size_t pi = (size_t)(it.first + (p < n ? p : 0)) * a.hq + h;  // p < n: in range
+        pm[p] = a.part_m[pi];
+        pl[p] = a.part_l[pi];
+        px[p] = ld4(a.part_acc + pi * a.head_dim + cc * 4);
+      }
       float M = -INFINITY;
-      for (int p = 0; p < it.nparts; p++) M = fmaxf(M, a.part_m[(size_t)(it.first + p) * a.hq + h]);
+#pragma unroll
+      for (int p = 0; p < kMergeRowsMaxParts; p++)
+        if (p < n) M = fmaxf(M, pm[p]);
       const float Ms = M == -INFINITY ? 0.0f : M;
       float L = 0.0f;
       float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int p = 0; p < it.nparts; p++) {
-        const size_t pi = (size_t)(it.first + p) * a.hq + h;
-        const float e = __builtin_amdgcn_exp2f(a.part_m[pi] - Ms);
-        L = fmaf(a.part_l[pi], e, L);
-        const float4 x = ld4(a.part_acc + pi * a.head_dim + cc * 4);
-        A.x = fmaf(x.x, e, A.x);
-        A.y = fmaf(x.y, e, A.y);
-        A.z = fmaf(x.z, e, A.z);
-        A.w = fmaf(x.w, e, A.w);
+#pragma unroll
+      for (int p = 0; p < kMergeRowsMaxParts; p++) {
+        if (p < n) {
+          const float e = __builtin_amdgcn_exp2f(pm[p] - Ms);
+          L = fmaf(pl[p], e, L);
+          A.x = fmaf(px[p].x, e, A.x);
+          A.y = fmaf(px[p].y, e, A.y);
+          A.z = fmaf(px[p].z, e, A.z);
+          A.w = fmaf(px[p].w, e, A.w);
+        }
       }
       const float inv = L == 0.0f ? 0.0f : 1.0f / L;
       r = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
@@ -565,7 +582,7 @@ hipError_t launch_merge(const MergeLaunch &a, int max_parts, hipStream_t s) {
   if (a.num_items <= 0) return hipSuccess;
   if (a.head_dim > 512 || (a.head_dim & 3)) return hipErrorInvalidValue;
   // Few partials per row: one row-wide workgroup per row; many: spread them over 4 or 16 waves.
-  if (max_parts <= 4)
+  if (max_parts <= kMergeRowsMaxParts)
     hipLaunchKernelGGL(merge_rows_kernel, dim3(a.num_items), dim3(256), 0, s, a);
   else if (max_parts <= 32)
     hipLaunchKernelGGL((merge_kernel<4>), dim3(a.num_items, a.hq), dim3(256), 0, s, a);
