@@ -47,14 +47,14 @@ def scheduler_state(seed, bs, chunk=None):
 
 
 @pytest.mark.parametrize("seed", range(12))
-@pytest.mark.parametrize("bs", [4, 16, 256])
+@pytest.mark.parametrize("bs", [4, 16, 256, 768])
 def test_prefill_matches_engine(seed, bs):
     _, seqs = scheduler_state(seed, bs, chunk=None if seed % 2 else 37)
     check_equal(S.build_prefill_metadata(seqs, bs), E.prepare_prefill(seqs, bs))
 
 
 @pytest.mark.parametrize("seed", range(12))
-@pytest.mark.parametrize("bs", [4, 16, 256])
+@pytest.mark.parametrize("bs", [4, 16, 256, 768])
 def test_decode_matches_engine(seed, bs):
     bm, seqs = scheduler_state(seed, bs)
     for s in seqs:
