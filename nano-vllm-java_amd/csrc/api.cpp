@@ -629,10 +629,12 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   // at 1024 (fewer partials to write and merge) and 6.96 / 6.84 TB/s at 8192 / 16384 (a
   // longer tail).
   // When even 64-key items leave fewer than 8 workgroups per CU (a small step), the largest
-  // chunk that still gives 2 per CU is taken instead: short items then cost more in fixed
-  // per-workgroup work and partials than they add in parallelism (Gemma3 global decode,
-  // 32 rows, 202 MB: 64.3 against 70.5 us for decode plus merge; C1 and the Gemma3 local
-  // layer keep 64).
+  // multiple of 64 keys that still gives every CU a workgroup is taken instead: short items
+  // cost more in fixed per-workgroup work and partials than they add in parallelism.  Measured
+  // after a flush (decode kernel, HIP events): Gemma3 global decode (32 rows, 202 MB) 41.7 us
+  // at 128 keys, 38.7 at 256, 38.3 at 384 (1.07 workgroups per CU; this rule's pick), 42.4 at
+  // 512; Qwen3 decode of 8 rows 12.3 us at 64, 11.8 at 128 (the pick); the Gemma3 local layer
+  // keeps 64.
   int64_t total = 0;
   for (const Row &r : rows) total += std::max(0, r.kend - r.kbeg);
   auto items_at = [&](int c) {
@@ -644,12 +646,20 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     return items * key.wg_per_item;
   };
   int chunk = 0;
-  for (int per_cu : {8, 2}) {
-    for (int c = 4096; c >= 64 && !chunk; c >>= 1)
-      if (items_at(c) >= (int64_t)ctx->num_cus * per_cu) chunk = c;
-    if (chunk) break;
+  for (int c = 4096; c >= 64 && !chunk; c >>= 1)
+    if (items_at(c) >= (int64_t)ctx->num_cus * 8) chunk = c;
+  if (!chunk) {
+    // items_at falls as the chunk grows: binary search over multiples of 64 in [64, 4096].
+    int lo = 1, hi = 64;  // in units of 64 keys; lo satisfies the bound or is the fallback
+    if (items_at(64) >= (int64_t)ctx->num_cus) {
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (items_at(64 * mid) >= (int64_t)ctx->num_cus) lo = mid;
+        else hi = mid - 1;
+      }
+    }
+    chunk = 64 * lo;
   }
-  if (!chunk) chunk = 64;
   // A paged item of `chunk` keys spans at most (chunk - 1) / BS + 2 pages; the row kernel
   // stages at most kRowTablePages of them.
   if (key.paged) chunk = std::min(chunk, (kRowTablePages - 1) * key.block_size);
