@@ -444,9 +444,11 @@ __global__ void __launch_bounds__(256) merge_rows_kernel(MergeLaunch a) {
 }
 
 // Log-sum-exp merge of the chunk partials of split rows; rows with no visible key get zeros.
-// One workgroup of NW waves per (row, head): wave w folds partials w, w + NW, ... (four loads in
-// flight per lane), lane c holding float4 c (and c + 64 at d = 512) of the head; the waves'
-// (m, l, acc) are then combined in wave order through LDS, so the result is deterministic.
+// One workgroup of NW waves per (row, head): wave w folds partials w, w + NW, ... in batches of
+// four whose loads are all issued before any is used (an online fold: the running sums are
+// rescaled when a batch raises the maximum), lane c holding float4 c (and c + 64 at d = 512)
+// of the head; the waves' (m, l, acc) are then combined in wave order through LDS, so the
+// result is deterministic.
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) merge_kernel(MergeLaunch a) {
   __shared__ float sm[NW], sl[NW];
@@ -461,39 +463,43 @@ __global__ void __launch_bounds__(NW * 64) merge_kernel(MergeLaunch a) {
     for (int c = threadIdx.x; c < d4; c += blockDim.x) out[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     return;
   }
-  // Pass 1: this wave's max over its partials.
-  float M = -INFINITY;
-  for (int p = wave; p < it.nparts; p += NW)
-    M = fmaxf(M, a.part_m[(size_t)(it.first + p) * a.hq + h]);
-  const float Ms = M == -INFINITY ? 0.0f : M;
-  float L = 0.0f;
+  float M = -INFINITY, L = 0.0f;
   float4 A0 = make_float4(0.f, 0.f, 0.f, 0.f), A1 = A0;
   const bool c0 = lane < d4, c1 = lane + 64 < d4;
   for (int p0 = wave; p0 < it.nparts; p0 += 4 * NW) {
-    float e[4];
+    float pm[4], pl[4];
     float4 x0[4], x1[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int p = p0 + NW * u;
       const bool ok = p < it.nparts;
-      const size_t pi = (size_t)(it.first + (ok ? p : p0)) * a.hq + h;
-      e[u] = ok ? __builtin_amdgcn_exp2f(a.part_m[pi] - Ms) : 0.0f;
-      L = fmaf(ok ? a.part_l[pi] : 0.0f, e[u], L);
+      const size_t pi = (size_t)(it.first + (ok ? p : p0)) * a.hq + h;  // p0 < nparts
       const float4 *src = reinterpret_cast<const float4 *>(a.part_acc + pi * a.head_dim);
-      x0[u] = c0 ? src[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-      x1[u] = c1 ? src[lane + 64] : make_float4(0.f, 0.f, 0.f, 0.f);
+      pm[u] = ok ? a.part_m[pi] : -INFINITY;
+      pl[u] = ok ? a.part_l[pi] : 0.0f;
+      x0[u] = ok && c0 ? src[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+      x1[u] = ok && c1 ? src[lane + 64] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    const float Mn = fmaxf(fmaxf(M, fmaxf(pm[0], pm[1])), fmaxf(pm[2], pm[3]));
+    const float Ms = Mn == -INFINITY ? 0.0f : Mn;
+    const float alpha = __builtin_amdgcn_exp2f(M - Ms);  // 0 while M is -inf
+    L *= alpha;
+    A0 = make_float4(A0.x * alpha, A0.y * alpha, A0.z * alpha, A0.w * alpha);
+    A1 = make_float4(A1.x * alpha, A1.y * alpha, A1.z * alpha, A1.w * alpha);
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      A0.x = fmaf(x0[u].x, e[u], A0.x);
-      A0.y = fmaf(x0[u].y, e[u], A0.y);
-      A0.z = fmaf(x0[u].z, e[u], A0.z);
-      A0.w = fmaf(x0[u].w, e[u], A0.w);
-      A1.x = fmaf(x1[u].x, e[u], A1.x);
-      A1.y = fmaf(x1[u].y, e[u], A1.y);
-      A1.z = fmaf(x1[u].z, e[u], A1.z);
-      A1.w = fmaf(x1[u].w, e[u], A1.w);
+      const float e = __builtin_amdgcn_exp2f(pm[u] - Ms);  // 0 for the unused slots
+      L = fmaf(pl[u], e, L);
+      A0.x = fmaf(x0[u].x, e, A0.x);
+      A0.y = fmaf(x0[u].y, e, A0.y);
+      A0.z = fmaf(x0[u].z, e, A0.z);
+      A0.w = fmaf(x0[u].w, e, A0.w);
+      A1.x = fmaf(x1[u].x, e, A1.x);
+      A1.y = fmaf(x1[u].y, e, A1.y);
+      A1.z = fmaf(x1[u].z, e, A1.z);
+      A1.w = fmaf(x1[u].w, e, A1.w);
     }
+    M = Mn;
   }
   if (lane == 0) {
     sm[wave] = M;
