@@ -242,6 +242,9 @@ __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
   }
 }
 
+// Row iterations a workgroup of rope_rows_kernel loads together.
+constexpr int kRopeRowsPerLoad = 4;
+
 // The same work with one group of LPR lanes per head row (q, k or v row of one token) and no
 // LDS or barriers.  Workgroup (t, s) handles token t's rows: row group g takes rows
 // g + RPB * i for the iterations i of slice s (the host sizes the slices so that small batches
@@ -255,7 +258,7 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
   constexpr int D = 4 * LPR * VPL;
   constexpr int HALF = D / 2;
   constexpr int RPB = 256 / LPR;  // row groups per workgroup
-  constexpr int NR = 4;           // rows loaded together
+  constexpr int NR = kRopeRowsPerLoad;  // rows loaded together
   const int t = blockIdx.x;
   const int c = threadIdx.x % LPR;
   const int grp = threadIdx.x / LPR;
@@ -468,9 +471,10 @@ hipError_t launch_rows(const RopeStoreLaunch &a, hipStream_t s, int num_cus) {
   if (rows <= 0) return hipSuccess;
   constexpr int RPB = 256 / LPR;
   const int iters = (rows + RPB - 1) / RPB;
-  // Split a token's rows over several workgroups only when the batch alone would leave the
-  // chip short of about four workgroups per CU.
-  int slices = 1;
+  // Split a token's rows over several workgroups when the batch alone would leave the chip
+  // short of about four workgroups per CU, and so that no workgroup loads more than one batch
+  // of row iterations (Qwen3-4B-like heads, 48 rows per token: 38.4 -> 36.8 us for 2112 tokens).
+  int slices = (iters + kRopeRowsPerLoad - 1) / kRopeRowsPerLoad;
   while (slices < iters && (int64_t)a.tokens * slices < 4LL * num_cus) slices++;
   RopeStoreLaunch b = a;
   b.iters_per_wg = (iters + slices - 1) / slices;
