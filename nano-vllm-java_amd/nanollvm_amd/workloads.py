@@ -211,10 +211,20 @@ def qwen3_decode_large_share(ways=8, by="head", seed=0, batch=256, lo=128, hi=32
 
 
 def qwen3_4b_mixed(seed=0, chunks=4, chunk=512, prior_hi=4096, rows=64, ctx_lo=4096,
-                   ctx_hi=16384) -> Workload:
+                   ctx_hi=16384, part="both") -> Workload:
+    """The mixed step; part="rows" keeps only its decode rows (a decode step), part="chunks"
+    only its prefill chunks (a prefill step), with the same draws."""
     rng = np.random.default_rng(seed)
     prior = uniform_lengths(rng, chunks, 0, prior_hi)
     dec = uniform_lengths(rng, rows, ctx_lo, ctx_hi)
+    if part == "rows":
+        return build(f"qwen3-4b-like mixed step, its {rows} decode rows alone",
+                     [(c - 1, 1) for c in dec], is_prefill=False, hq=32, hkv=8, d=128,
+                     scale=QWEN_SCALE, rng=rng)
+    if part == "chunks":
+        return build(f"qwen3-4b-like mixed step, its {chunks}x{chunk} prefill chunks alone",
+                     [(p, chunk) for p in prior], is_prefill=True, hq=32, hkv=8, d=128,
+                     scale=QWEN_SCALE, rng=rng)
     seqs = [(p, chunk) for p in prior] + [(c - 1, 1) for c in dec]
     return build(f"qwen3-4b-like mixed: {chunks}x{chunk} prefill chunks (prior U[0,{prior_hi}]) "
                  f"+ {rows} decode rows ctx U[{ctx_lo},{ctx_hi}]", seqs, is_prefill=True, hq=32,
