@@ -113,11 +113,13 @@ def _norm_heads(x, w, one_plus):
 
 
 def check_fused(ctx, case, name, q_w, k_w, one_plus=False, v_norm=False, max_pos=None,
-                theta=1e4, outputs=True, norms=True):
+                theta=1e4, outputs=True, norms=True, twin=False):
     """The per-head norms + RoPE + Attention.forward chain through nva_norm_rope_attention_forward
     against the oracle chain (normHeads, RoPE, Attention.forward): rotated q/k (when `outputs`)
     and every page byte bit-exact, attention within the bar.  norms=False passes no q/k norm at
-    all (RoPE only); outputs=False passes no q_out/k_out."""
+    all (RoPE only); outputs=False passes no q_out/k_out.  twin (with outputs=False): the same
+    call again with q_out/k_out given must return bit-identical attention and the oracle's
+    rotated q, bit for bit (whether the caller asks for the rotated rows changes nothing)."""
     wl = case.wl
     say(f"{name}: tokens={wl.tokens} hq={wl.hq} hkv={wl.hkv} d={wl.d} W={wl.window} "
         f"bs={wl.block_size} one_plus={one_plus} v_norm={v_norm} outputs={outputs}")
@@ -139,6 +141,7 @@ def check_fused(ctx, case, name, q_w, k_w, one_plus=False, v_norm=False, max_pos
         vn = RMSNorm.weightless(EPS) if v_norm else None
         q_out = torch.empty(case.q.shape, dtype=torch.float32, device="cuda") if outputs else None
         k_out = torch.empty(case.k.shape, dtype=torch.float32, device="cuda") if outputs else None
+        q_in, k_in, v_in = case.q, case.k, case.v
         out = attn.forward_with_norm_rope(rope, wl.meta.positions, dev(case.q), dev(case.k),
                                           dev(case.v), ctx, q_norm=qn, k_norm=kn, v_norm=vn,
                                           q_out=q_out, k_out=k_out)
@@ -163,6 +166,17 @@ def check_fused(ctx, case, name, q_w, k_w, one_plus=False, v_norm=False, max_pos
         if case.paged:
             assert np.array_equal(bits(arena.get_key_cache(0)), bits(kc)), "K pages differ"
             assert np.array_equal(bits(arena.get_value_cache(0)), bits(vc)), "V pages differ"
+        if twin and not outputs:
+            # Stores the same rows to the same slots again, so the pages do not change.
+            q_out = torch.empty(case.q.shape, dtype=torch.float32, device="cuda")
+            k_out = torch.empty(case.k.shape, dtype=torch.float32, device="cuda")
+            out2 = attn.forward_with_norm_rope(rope, wl.meta.positions, dev(q_in), dev(k_in),
+                                               dev(v_in), ctx, q_norm=qn, k_norm=kn,
+                                               v_norm=vn, q_out=q_out, k_out=k_out)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(q_out.cpu().numpy()), bits(qr)), "q not bit-exact"
+            assert np.array_equal(bits(out2.cpu().numpy()), bits(got)), \
+                "attention differs when the rotated q/k are asked for"
     finally:
         ctx.clear()
         arena.close()
