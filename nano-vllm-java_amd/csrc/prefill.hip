@@ -14,9 +14,12 @@
 // XCDs share, so slots need no XCD-aware placement.  A segment is a tile of 16 * 8 / HPW queries of one
 // sequence for HPW query heads of one KV head, over a key range [ks, ke).  The 8 waves of the
 // workgroup each own 16 queries of one head.
-//   * Key tiles of 32 rows of K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
-//     register staging), double-buffered so the next tile streams in while this one is used;
-//     one barrier per tile.  Rows are stored unpadded; K rows have their 16-byte chunks
+//   * Key tiles of 32 rows of K and V are copied HBM -> LDS with 16-byte loads that write LDS
+//     directly (no register staging), double-buffered so the next tile streams in while this
+//     one is used; one barrier per tile.  A full tile inside one page (or of dense rows) is 32
+//     consecutive rows: its copies are buffer loads from a wave-uniform descriptor plus fixed
+//     32-bit lane offsets, no per-lane address arithmetic; the last tile of a chunk and tiles
+//     that cross a page compute each row's address (rows past the chunk clamped).  Rows are stored unpadded; K rows have their 16-byte chunks
 //     XOR-swizzled (kswz) so the column reads of QK are conflict-free, V rows are read
 //     along the row and need no swizzle.  The block ids of the segment's pages are staged in LDS
 //     once, so a paged tile load never waits on a global table read.
@@ -43,6 +46,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+// Word 3 of a raw (stride 0) buffer descriptor on gfx9-family parts: 32-bit data format, no
+// swizzle; out-of-range offsets read zero.
+constexpr int kBufferWord3 = 0x00020000;
 constexpr float kLazyRescale = 8.0f;  // log2 units
 
 }  // namespace
@@ -97,6 +103,17 @@ __device__ __forceinline__ int kswz(int c, int r) {
   return c ^ x;
 }
 
+// 16 bytes per lane from base + off to LDS (lane l's at lds + 4 l), through a buffer
+// descriptor over [base, base + bytes): the base stays in scalar registers, the lane offset is
+// 32-bit, and the hardware range-checks the read (reads past `bytes` return zeros).
+__device__ __forceinline__ void copy16_to_lds(const float *base, int bytes, uint32_t off,
+                                              float *lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, bytes,
+                                        kBufferWord3),
+      (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
+}
+
 // Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the block
 // table, which starts at page blk0.
 __device__ __forceinline__ int64_t tile_row(const KvView &kv, const int32_t *stab, int blk0,
@@ -138,6 +155,22 @@ prefill_kernel(TileLaunch a) {
 
   const int slot = blockIdx.x;
   const int seg_end = a.seg_off[slot + 1];
+  // Byte offsets of this lane's copies within a tile whose 32 rows are consecutive rows of the
+  // K/V arrays (every full tile of a dense step, and of a paged one when it lies in one page):
+  // such a tile is copied from one wave-uniform base plus these fixed offsets.
+  uint32_t koff[LPW], voff[LPW];
+  {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t rsb = (uint32_t)(a.hkv * D) * 4u;
+#pragma unroll
+    for (int p = 0; p < LPW; p++) {
+      const int q = (p * NW + wave) * 64 + lane;  // chunk q of the tile, row-major
+      const int r = q / C4, pos = q - r * C4;
+      koff[p] = (uint32_t)r * rsb + (uint32_t)kswz<D>(pos, r) * 16u;
+      voff[p] = (uint32_t)r * rsb + (uint32_t)pos * 16u;
+    }
+  }
   for (int seg = a.seg_off[slot]; seg < seg_end; seg++) {
   // Every wave is done with the previous segment's LDS tiles and table before they are reused.
   __syncthreads();
@@ -173,12 +206,16 @@ prefill_kernel(TileLaunch a) {
   const int whi_max = off + wq1 + 1;
 
   // Q^T operand: lane (i, g) holds Q[query i][DQ*g + s], s < DQ, for the whole key loop.
+  // Read from a wave-uniform row base plus a 32-bit lane offset (queries past the sequence
+  // read its last one; a wave with none reads that one too).
   float qr[DQ];
   {
-    const float *qp = a.q + ((size_t)(it.qstart + qic) * a.hq + h) * D + DQ * g;
+    const int wq0c = min(wq0, it.qlen - 1);
+    const float *qw = a.q + ((size_t)(it.qstart + wq0c) * a.hq + h) * D;
+    const uint32_t lo = (uint32_t)(qic - wq0c) * (uint32_t)(a.hq * D) + (uint32_t)(DQ * g);
 #pragma unroll
     for (int s = 0; s < DQ; s += 4) {
-      const float4 x = ld4(qp + s);
+      const float4 x = ld4(qw + lo + s);
       qr[s] = x.x;
       qr[s + 1] = x.y;
       qr[s + 2] = x.z;
@@ -210,7 +247,37 @@ prefill_kernel(TileLaunch a) {
   // i.e. position q % C4 of tile row q / C4.
   const int lrow = C4 <= 64 ? lane / C4 : 0;  // rows within one instruction (d <= 256)
   const int lpos = C4 <= 64 ? lane - lrow * C4 : 0;
+  int cur_page = -1;  // page whose block id cur_id holds (wave-uniform)
+  int cur_id = 0;
   auto issue_tile = [&](int kt, float *dk, float *dv) {
+    // A full tile inside one page (or of dense rows): one uniform row base, fixed offsets.
+    if (kt + KT <= it.ke &&
+        (!a.kv.paged || (a.kv.bs_shift >= 0 && (kt >> a.kv.bs_shift) ==
+                                                   ((kt + KT - 1) >> a.kv.bs_shift)))) {
+      int64_t row0;
+      if (!a.kv.paged) {
+        row0 = (int64_t)it.kbase + kt;
+      } else {
+        const int pg = kt >> a.kv.bs_shift;
+        if (pg != cur_page) {
+          cur_id = __builtin_amdgcn_readfirstlane(stab[pg - blk0]);
+          cur_page = pg;
+        }
+        row0 = (int64_t)cur_id * a.kv.block_size + (kt - (pg << a.kv.bs_shift));
+      }
+      const int tile_bytes = KT * (int)rs * 4;
+      const float *gk0 = kbase + row0 * (int64_t)rs;
+      const float *gv0 = vbase + row0 * (int64_t)rs;
+#pragma unroll
+      for (int p = 0; p < LPW; p++) {
+        const int gi = p * NW + wave;
+        copy16_to_lds(gk0, tile_bytes, koff[p], dk + gi * 256);
+        copy16_to_lds(gv0, tile_bytes, voff[p], dv + gi * 256);
+      }
+      return;
+    }
+    // Last (partial) tile, or one that crosses a page: per-row addresses, rows past the chunk
+    // clamped to its last key.
 #pragma unroll
     for (int p = 0; p < LPW; p++) {
       const int gi = p * NW + wave;
