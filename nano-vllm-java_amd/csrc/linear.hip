@@ -19,10 +19,11 @@
 //     read the same way: for each 8-wide K chunk a lane (i, h) reads one float4 of its row
 //     (elements 4h .. 4h + 3), which feeds 4 MFMA steps -- step s contracts k = 4h + s, a
 //     permutation of the chunk that A and B share.
-//   * K tiles of 32 are copied HBM -> LDS with global_load_lds_dwordx4, double-buffered, one
-//     barrier per tile; each 128-byte row of a tile has its 16-byte chunks XOR-swizzled by
-//     ((row >> 1) & 7): measured free of LDS bank conflicts (row & 7: half of the LDS-active
-//     cycles were conflict stalls).
+//   * K tiles of 32 are copied HBM -> LDS with 16-byte loads that write LDS directly (buffer
+//     loads from a uniform descriptor for interior tiles), double-buffered, one barrier per
+//     tile; each 128-byte row of a tile has its 16-byte chunks XOR-swizzled by ((row >> 1) & 7):
+//     measured free of LDS bank conflicts (row & 7: half of the LDS-active cycles were conflict
+//     stalls).
 //   * Output block layout (32 x 32, 16 values per lane): value r of lane (i, h) is row
 //     8 * (r / 4) + 4 * h + r % 4, column i -- lanes 0..31 write 128 contiguous bytes.
 //   * When the grid alone cannot fill the chip, K is split over blockIdx.z (both MFMA
@@ -32,6 +33,7 @@
 //     separate launch.)
 // Algorithmic work: 2 * M * N * K flops; HBM bytes (once): 4 * (M * K + N * K + M * N).
 #include "nva_internal.h"
+#include "nva_device.h"
 
 namespace nva {
 
@@ -102,7 +104,29 @@ linear_kernel(LinearLaunch a) {
   // row 8g + l / 8, LDS chunk position l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7).
   const int lrow = lane >> 3;
   const int lpos = lane & 7;
+  // An interior tile (all 128 rows of x and of W exist, and the K tile lies inside the slice)
+  // is copied from a wave-uniform base at (row m0 or n0, column kt) plus these fixed byte
+  // offsets, through buffer descriptors: no per-lane address arithmetic.
+  const bool interior = m0 + BM <= a.m && n0 + BN <= a.n;
+  uint32_t loff[LPW];
+#pragma unroll
+  for (int p = 0; p < LPW; p++) {
+    const int r = 8 * (NW * p + wave) + lrow;
+    loff[p] = (uint32_t)r * (uint32_t)a.k * 4u + (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+  }
+  const int span_bytes = ((BM - 1) * a.k + BK) * 4;  // rows m0.. (n0..), columns kt..kt+BK-1
   auto issue = [&](int kt, float *da, float *db) {
+    if (interior && kt + BK <= ke) {
+      const float *xb = a.x + (size_t)m0 * a.k + kt;
+      const float *wb = a.w + (size_t)n0 * a.k + kt;
+#pragma unroll
+      for (int p = 0; p < LPW; p++) {
+        const int g = NW * p + wave;
+        copy16_to_lds(xb, span_bytes, loff[p], da + g * 8 * BK);
+        copy16_to_lds(wb, span_bytes, loff[p], db + g * 8 * BK);
+      }
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < LPW; p++) {
       const int g = NW * p + wave;

@@ -38,6 +38,7 @@
 //   * Only tiles that cross the causal diagonal, the window edge or the end of the keys are
 //     masked.
 #include "nva_internal.h"
+#include "nva_device.h"
 
 namespace nva {
 
@@ -46,9 +47,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-// Word 3 of a raw (stride 0) buffer descriptor on gfx9-family parts: 32-bit data format, no
-// swizzle; out-of-range offsets read zero.
-constexpr int kBufferWord3 = 0x00020000;
 constexpr float kLazyRescale = 8.0f;  // log2 units
 
 }  // namespace
@@ -101,17 +99,6 @@ __device__ __forceinline__ int kswz(int c, int r) {
   int x = r & 7;
   if constexpr (GS >= 16) x |= ((c >> 4) & 1) << 3;
   return c ^ x;
-}
-
-// 16 bytes per lane from base + off to LDS (lane l's at lds + 4 l), through a buffer
-// descriptor over [base, base + bytes): the base stays in scalar registers, the lane offset is
-// 32-bit, and the hardware range-checks the read (reads past `bytes` return zeros).
-__device__ __forceinline__ void copy16_to_lds(const float *base, int bytes, uint32_t off,
-                                              float *lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, bytes,
-                                        kBufferWord3),
-      (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
 }
 
 // Row of key t: dense rows follow kbase; paged rows go through the LDS copy of the block

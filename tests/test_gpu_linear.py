@@ -86,6 +86,8 @@ def check(got, want, name):
     (130, 2048, 1024, False),  # M tail past one 128-row tile
     (256, 2048, 1024, True),   # 256-row decode batch: 256 blocks, one per CU
     (384, 2048, 1024, True),   # more blocks than CUs: the 128 x 128 tiles
+    (384, 1028, 1000, True),   # tiles: interior and edge tiles side by side, ragged N and K
+    (300, 4100, 520, False),   # tiles: M and N tails, K % 32 == 4 (last K tile per-lane copied)
 ])
 def test_linear_matches_oracle(ctx, rows, inf, outf, bias):
     x, w, b = data(rows, inf, outf, bias, rows + inf)
