@@ -107,7 +107,8 @@ linear_kernel(LinearLaunch a) {
   // An interior tile (all 128 rows of x and of W exist, and the K tile lies inside the slice)
   // is copied from a wave-uniform base at (row m0 or n0, column kt) plus these fixed byte
   // offsets, through buffer descriptors: no per-lane address arithmetic.
-  const bool interior = m0 + BM <= a.m && n0 + BN <= a.n;
+  // (Offsets and the descriptor size are 32-bit: 128 rows of k floats must stay below 2 GiB.)
+  const bool interior = m0 + BM <= a.m && n0 + BN <= a.n && a.k < (1 << 22);
   uint32_t loff[LPW];
 #pragma unroll
   for (int p = 0; p < LPW; p++) {
