@@ -237,8 +237,9 @@ prefill_kernel(TileLaunch a) {
   int cur_page = -1;  // page whose block id cur_id holds (wave-uniform)
   int cur_id = 0;
   auto issue_tile = [&](int kt, float *dk, float *dv) {
-    // A full tile inside one page (or of dense rows): one uniform row base, fixed offsets.
-    if (kt + KT <= it.ke &&
+    // A full tile inside one page (or of dense rows): one uniform row base, fixed offsets
+    // (32-bit: the tile's rows must span less than 2 GiB).
+    if (kt + KT <= it.ke && rs < (size_t)(1 << 22) &&
         (!a.kv.paged || (a.kv.bs_shift >= 0 && (kt >> a.kv.bs_shift) ==
                                                    ((kt + KT - 1) >> a.kv.bs_shift)))) {
       int64_t row0;
