@@ -284,8 +284,29 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
   // the edge copy the last valid row (their sums are not stored); chunks past the wave's K
   // range copy a valid address and are zeroed at use.
   const int lrow = lane >> 3, lpos = lane & 7;
+  // A full block (32 rows of x and of W) and a stage inside the wave's K range: copied from
+  // wave-uniform bases (row m0 / n0, column kt) plus fixed byte offsets, shared by x and W
+  // (both K-contiguous with row stride k), through buffer descriptors.
+  const bool full_block = m0 + 32 <= a.m && n0 + 32 <= a.n && a.k < (1 << 22);
+  uint32_t soff[4];
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const int r = 8 * g + lrow;
+    soff[g] = (uint32_t)r * (uint32_t)a.k * 4u + (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+  }
+  const int span_bytes = (31 * a.k + KI) * 4;
   auto issue = [&](int it, int st) {
     const int kt = wk0 + it * KI;
+    if (full_block && kt + KI <= wk1) {
+      const float *xb = a.x + (size_t)m0 * a.k + kt;
+      const float *wb = a.w + (size_t)n0 * a.k + kt;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        copy16_to_lds(xb, span_bytes, soff[g], &ring[w][st][0][g * 8 * KI]);
+        copy16_to_lds(wb, span_bytes, soff[g], &ring[w][st][1][g * 8 * KI]);
+      }
+      return;
+    }
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       const int r = 8 * g + lrow;
