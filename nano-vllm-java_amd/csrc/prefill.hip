@@ -19,10 +19,11 @@
 //     one is used; one barrier per tile.  A full tile inside one page (or of dense rows) is 32
 //     consecutive rows: its copies are buffer loads from a wave-uniform descriptor plus fixed
 //     32-bit lane offsets, no per-lane address arithmetic; the last tile of a chunk and tiles
-//     that cross a page compute each row's address (rows past the chunk clamped).  Rows are stored unpadded; K rows have their 16-byte chunks
-//     XOR-swizzled (kswz) so the column reads of QK are conflict-free, V rows are read
-//     along the row and need no swizzle.  The block ids of the segment's pages are staged in LDS
-//     once, so a paged tile load never waits on a global table read.
+//     that cross a page compute each row's address (rows past the chunk clamped).  Rows are
+//     stored unpadded; K rows have their 16-byte chunks XOR-swizzled (kswz) so the column
+//     reads of QK are conflict-free, V rows are read along the row and need no swizzle.  The
+//     block ids of the segment's pages are staged in LDS once, so a paged tile load never
+//     waits on a global table read.
 //   * Per tile each wave computes (D = 128)
 //       S^T[key][query] = K Q^T      64 x v_mfma_f32_16x16x4_f32, K from LDS (ds_read_b128),
 //                                    Q (16 queries x D/4 per lane) resident in registers;
