@@ -69,3 +69,27 @@ def test_long_rows_small_pages(ctx, block_size, is_prefill):
                  is_prefill=is_prefill, hq=4, hkv=2, d=128, scale=float(np.float32(128 ** -0.5)),
                  rng=rng, block_size=block_size, pool_cap=20000)
     check_attention(ctx, Case(wl, seed=block_size + 3), wl.name)
+
+
+@pytest.mark.parametrize("block_size", [32, 64, 128])
+@pytest.mark.parametrize("window", [0, 45])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_tile_copies_across_pages(ctx, d, block_size, window):
+    """Pages of one to four 32-key tiles: a full tile inside one page is copied from one row
+    base (its block id re-read only when the page changes), while the chunk's last tile and tiles
+    that a window start or a mid-page chunk start moves across a page boundary take per-row
+    addresses.  Ragged sequences mix both kinds in every segment; the window of 45 keys starts
+    tiles off the 32-key grid."""
+    rng = np.random.default_rng(d + block_size + window)
+    seqs = [(block_size * 3, 150), (block_size // 2 + 7, 97), (0, 260), (5 * block_size + 3, 33)]
+    wl = W.build(f"tile copies d{d} bs{block_size} w{window}", seqs, is_prefill=True, hq=4,
+                 hkv=2, d=d, scale=float(np.float32(d ** -0.5)), window=window, rng=rng,
+                 block_size=block_size)
+    ctx.reset_stats()
+    ctx.set_timing(True)
+    try:
+        check_attention(ctx, Case(wl, seed=d * 3 + block_size), wl.name)
+        launches, _ = ctx.kernel_stats("prefill")
+    finally:
+        ctx.set_timing(False)
+    assert launches >= 1, "the MFMA prefill kernel did not run"
