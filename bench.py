@@ -51,9 +51,9 @@ def parse():
                     help="write 512 MB between steps so K/V that fits the 256 MB Infinity Cache "
                          "is read from HBM (kernel timings exclude the flush)")
     ap.add_argument("--linear-vs-vendor", action="store_true",
-                    help="time o_proj (nva_linear_forward on the context's backend and on the "
-                         "library's own kernels) and torch.addmm (hipBLASLt) on the decode and "
-                         "prefill o_proj shapes, one JSON line per shape")
+                    help="time o_proj (nva_linear_forward, the library's own kernels) and "
+                         "torch.addmm (hipBLASLt) on the decode and prefill o_proj shapes, one "
+                         "JSON line per shape")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy three times (the "
                          "known-size reference for the FETCH_SIZE/WRITE_SIZE counters)")
@@ -305,42 +305,37 @@ def time_step_plan(ctx, wl, step, reps=20):
             "plans_per_step": round(nb / reps, 2)}
 
 
-def linear_backend():
-    """The o_proj backend contexts are created with (NVA_LINEAR_BACKEND, default auto)."""
-    return os.environ.get("NVA_LINEAR_BACKEND", "auto")
-
-
-def native_linear_context():
-    """A context whose o_proj runs this library's own kernels for every shape."""
-    from nanollvm_amd import Context
-    old = os.environ.get("NVA_LINEAR_BACKEND")
-    os.environ["NVA_LINEAR_BACKEND"] = "native"
-    try:
-        return Context(0)
-    finally:
-        if old is None:
-            del os.environ["NVA_LINEAR_BACKEND"]
-        else:
-            os.environ["NVA_LINEAR_BACKEND"] = old
-
-
-def o_proj_kernel(m, n, backend):
+def o_proj_kernel(m, n):
+    """The library kernel nva_linear_forward runs for an [m, K] x [n, K]^T o_proj."""
     import torch
     blocks = ((n + 31) // 32) * ((m + 31) // 32)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if backend == "vendor" or (backend == "auto" and m > 8 and blocks > cus):
-        return "hipBLASLt (fp32 compute, bias epilogue)"
     if m <= 8:
         return "gemv_kernel (weight-streaming GEMV, <= 8 rows)"
     if blocks <= cus:
         return "skinny_kernel<8,2> (fp32 MFMA 32x32x2, one 32x32 block per workgroup, K over 8 waves)"
-    return "linear_kernel (fp32 MFMA 32x32x2, 128x128 tiles; K slices from a per-CU cost model)"
+    return "linear_kernel (fp32 MFMA 32x32x2, 128x64 tiles, two workgroups per CU; K slices from a per-CU cost model)"
+
+
+def time_calls(fn, steps, warmup):
+    """ms per call of `steps` back-to-back calls, between two HIP events on torch's current
+    stream (the stream the library's context runs on), after `warmup` calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def time_o_proj(ctx, attn_out, wl, steps, warmup, hidden=1024, seed=21):
     """o_proj (Linear.Row, Qwen3-0.6B: [hidden, Hq * d] weight) on this step's attention output,
-    timed like the step, on the context's backend and (under "native") on this library's own
-    kernels.  Reported beside the step, not inside its value."""
+    timed over back-to-back calls.  Reported beside the step, not inside its value."""
     import torch
     from nanollvm_amd import Linear
     g = torch.Generator(device="cuda")
@@ -352,54 +347,28 @@ def time_o_proj(ctx, attn_out, wl, steps, warmup, hidden=1024, seed=21):
     m = x.shape[0]
     flops = 2.0 * m * hidden * k
     byts = 4.0 * (m * k + hidden * k + m * hidden)
-
-    def timed(c):
-        for _ in range(warmup):
-            lin.forward(x, c)
-        torch.cuda.synchronize()
-        c.reset_stats()
-        c.set_timing(True)
-        for _ in range(steps):
-            lin.forward(x, c)
-        torch.cuda.synchronize()
-        c.set_timing(False)
-        n, t = c.kernel_stats("linear")
-        return t / max(n, 1)
-
-    ms = timed(ctx)
+    ms = time_calls(lambda: lin.forward(x, ctx), max(steps, 20), warmup)
     tf = flops / (ms * 1e-3) / 1e12
-    res = {"kernel": o_proj_kernel(m, hidden, linear_backend()),
-           "shape": f"[{m}, {k}] x [{hidden}, {k}]^T", "ms": round(ms, 5),
-           "tflops": round(tf, 2), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-           "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}
-    if o_proj_kernel(m, hidden, linear_backend()) != o_proj_kernel(m, hidden, "native"):
-        nctx = native_linear_context()
-        try:
-            nms = timed(nctx)
-        finally:
-            nctx.close()
-        ntf = flops / (nms * 1e-3) / 1e12
-        res["native"] = {"kernel": o_proj_kernel(m, hidden, "native"), "ms": round(nms, 5),
-                         "tflops": round(ntf, 2),
-                         "mfma_frac": round(ntf / FP32_MFMA_PEAK_TFLOPS, 4)}
-    return res
+    return {"kernel": o_proj_kernel(m, hidden), "shape": f"[{m}, {k}] x [{hidden}, {k}]^T",
+            "ms": round(ms, 5), "tflops": round(tf, 2),
+            "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}
 
 
 # o_proj shapes of Qwen3-0.6B (hidden 1024, Hq * d = 2048): decode batches and the 4096-token
-# prefill step.
+# prefill step; and of the Qwen3-4B-like mixed step (hidden 2560, Hq * d = 4096).
 LINEAR_SHAPES = [(1, 2048, 1024), (8, 2048, 1024), (64, 2048, 1024), (128, 2048, 1024),
-                 (256, 2048, 1024), (4096, 2048, 1024)]
+                 (256, 2048, 1024), (4096, 2048, 1024), (2112, 4096, 2560)]
 
 
 def linear_vs_vendor(args, ctx):
-    """nva_linear_forward (on the context's backend, and on this library's own kernels) against
-    torch.addmm (hipBLASLt) on the same fp32 operands, all timed with HIP events over `steps`
-    back-to-back calls after `warmup`; max-abs error of each against a float64 product."""
+    """nva_linear_forward against torch.addmm (hipBLASLt) on the same fp32 operands, both timed
+    over `steps` back-to-back calls after `warmup`; max-abs error of each against a float64
+    product."""
     import torch
     from nanollvm_amd import Linear
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
-    nctx = native_linear_context()
     for m, k, n in LINEAR_SHAPES:
         x = torch.randn((m, k), device="cuda", generator=g)
         w = torch.randn((n, k), device="cuda", generator=g) / math.sqrt(k)
@@ -409,24 +378,13 @@ def linear_vs_vendor(args, ctx):
         wt = w.T
         res = {}
         for name, fn in (("nva", lambda: lin.forward(x, ctx)),
-                         ("nva_native", lambda: lin.forward(x, nctx)),
                          ("hipblaslt", lambda: torch.addmm(bias, x, wt))):
             y = fn()
-            for _ in range(args.warmup):
-                fn()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(args.steps):
-                fn()
-            e1.record()
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / args.steps
+            ms = time_calls(fn, args.steps, args.warmup)
             res[name] = {"us": round(ms * 1e3, 2), "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 2),
                          "max_abs_vs_f64": float((y.double() - ref).abs().max())}
-        print(json.dumps({"shape": f"[{m}, {k}] x [{n}, {k}]^T", "backend": linear_backend(),
-                          "nva_kernel": o_proj_kernel(m, n, linear_backend()), **res}), flush=True)
-    nctx.close()
+        print(json.dumps({"shape": f"[{m}, {k}] x [{n}, {k}]^T", "nva_kernel": o_proj_kernel(m, n),
+                          **res}), flush=True)
 
 
 def kernel_a_roofline(wl, stats):

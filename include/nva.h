@@ -274,12 +274,10 @@ nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const fl
  * tensor/Ops.java:84-124 -> MatmulRuntime.linear, tensor/MatmulRuntime.java:234-255:
  * y[rows, out] = x[rows, in] weight[out, in]^T (+ bias[out]).  x, weight, bias and y are
  * DEVICE pointers (x and weight 16-byte aligned, in % 4 == 0); bias may be NULL.  x is
- * typically the attention output [tokens, num_heads * head_dim] used in place.  fp32 on MFMA;
- * the sum order differs from the reference's gemv panels (fp32 rounding only).  Up to 8 rows run
- * the library's weight-streaming GEMV and batches whose 32 x 32 output blocks fit one per CU its
- * block kernel; larger GEMMs run hipBLASLt (fp32 compute, the bias in its epilogue).
- * NVA_LINEAR_BACKEND, read when a context is created, overrides this: "native" runs the
- * library's own kernels for every shape, "vendor" hipBLASLt for every shape. */
+ * typically the attention output [tokens, num_heads * head_dim] used in place (in < 4194304).
+ * fp32 on MFMA; the sum order differs from the reference's gemv panels (fp32 rounding only).
+ * Up to 8 rows run the library's weight-streaming GEMV, batches whose 32 x 32 output blocks fit
+ * one per CU its block kernel, and larger GEMMs its 128 x 64-tile kernel. */
 nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
                               const float *weight, int out, const float *bias, float *y);
 

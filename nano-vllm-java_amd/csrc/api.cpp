@@ -46,8 +46,8 @@ namespace {
 
 // The scratch plan held by one device's array, so a call can skip copying the same plan again.
 struct ScratchTag {
-  uint64_t plan_id = 0;
-  size_t offset = 0;
+  uint64_t plan_id = 0;  // 0: no plan known to be held
+  size_t offset = 0, bytes = 0;
 };
 
 // Per device: its address of `scratch` (looked up once, under the mutex, with that device
@@ -242,10 +242,6 @@ struct nva_ctx {
   DevBuf d_k_rot;    // fused path scratch for rotated k
   DevBuf d_v_norm;   // fused path scratch for normalised v (dense prefill with a v norm)
   DevBuf d_lin;      // split-K partial sums of the linear kernel
-  // o_proj backend (NVA_LINEAR_BACKEND at context creation): auto = GEMV up to a few rows,
-  // hipBLASLt above; native = this library's kernels only; vendor = hipBLASLt for every shape.
-  enum LinearBackend { kLinearAuto, kLinearNative, kLinearVendor } linear_backend = kLinearAuto;
-  VendorGemm *gemm = nullptr;  // created on the first hipBLASLt call
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
 
   // This device's address of the no-allocation scratch array (null if the lookup failed).
@@ -782,71 +778,144 @@ KvView make_dense_view(const float *k, const float *v) {
   return view;
 }
 
-// The attention part of Attention.forward once the store (if any) is done.  With scr null the
-// plan and partials use the context's buffers; otherwise the scratch array's regions.
-nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &view,
-                         int num_blocks, const float *q, int num_tokens, float *out,
-                         Scratch *scr) {
+// The plan of one attention call (the descriptor, the step, and whether keys are paged over
+// an arena of num_blocks pages of block_size tokens or dense rows), plus the query heads per
+// workgroup of the row and tile kernels.
+nva_status attention_plan(nva_ctx *ctx, const nva_attn_desc &d, int paged, int block_size,
+                          int num_blocks, int num_tokens, Plan **plan, int *hpw_row,
+                          int *hpw_tile) {
   const int rep = d.num_heads / d.num_kv_heads;
-  const int hpw_row = largest_pow2_divisor_upto(rep, row_kernel_max_heads(d.head_dim));
+  *hpw_row = largest_pow2_divisor_upto(rep, row_kernel_max_heads(d.head_dim));
   // Query heads per prefill workgroup: at most a quarter of its waves, so a workgroup covers at
   // least 64 queries of each head (measured: Gemma3 d = 256 prefill 13% faster with 2 heads
   // than with 4, Gemma 4 d = 512 3% faster with 1 than with 4, Qwen3-4B shape 4% faster with 2
   // than with 4).
-  const int hpw_tile = largest_pow2_divisor_upto(rep, prefill_max_heads(d.head_dim));
-  const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, hpw_tile);
-  if (!row_kernel_supports(d.head_dim, hpw_row))
+  *hpw_tile = largest_pow2_divisor_upto(rep, prefill_max_heads(d.head_dim));
+  const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, *hpw_tile);
+  if (!row_kernel_supports(d.head_dim, *hpw_row))
     return fail(ctx, NVA_E_UNSUPPORTED, "head_dim %d has no row kernel in this build",
                 d.head_dim);
   PlanKey key;
   key.window = d.sliding_window > 0 ? d.sliding_window : 0;
   key.mfma = mfma ? 1 : 0;
-  key.tile_q = mfma ? prefill_tile_queries(d.head_dim, hpw_tile) : 0;
-  key.wg_per_item = d.num_kv_heads * (rep / hpw_row);
-  key.blocks_per_cu = mfma ? ctx_prefill_blocks_per_cu(ctx, d.head_dim, hpw_tile) : 0;
-  key.tile_groups = mfma ? d.num_kv_heads * (rep / hpw_tile) : 0;
+  key.tile_q = mfma ? prefill_tile_queries(d.head_dim, *hpw_tile) : 0;
+  key.wg_per_item = d.num_kv_heads * (rep / *hpw_row);
+  key.blocks_per_cu = mfma ? ctx_prefill_blocks_per_cu(ctx, d.head_dim, *hpw_tile) : 0;
+  key.tile_groups = mfma ? d.num_kv_heads * (rep / *hpw_tile) : 0;
   key.tokens = num_tokens;
-  key.paged = view.paged;
-  key.block_size = view.paged ? view.block_size : 0;
-  key.num_blocks = view.paged ? num_blocks : 0;
+  key.paged = paged;
+  key.block_size = paged ? block_size : 0;
+  key.num_blocks = paged ? num_blocks : 0;
   key.head_dim = d.head_dim;
   key.num_heads = d.num_heads;
   key.num_kv_heads = d.num_kv_heads;
+  return get_plan(ctx, key, plan);
+}
+
+// Regions of the no-allocation array one call uses: [gather rows | plan lists | partials],
+// each 256-byte aligned.
+struct ScratchLayout {
+  size_t plan_off = 0, part_off = 0, part_bytes = 0, end = 0;
+};
+
+ScratchLayout scratch_layout(size_t gather_bytes, const Plan &plan, const nva_attn_desc &d) {
+  ScratchLayout l;
+  const size_t parts = (size_t)plan.num_parts * d.num_heads;
+  l.plan_off = align256(gather_bytes);
+  l.part_off = align256(l.plan_off + plan.host.size());
+  l.part_bytes = parts * (2 + (size_t)d.head_dim) * sizeof(float);
+  l.end = l.part_off + l.part_bytes;
+  return l;
+}
+
+// A kernel is about to write [begin, end) of this device's array: the plan recorded as held
+// there no longer is, if the ranges meet.
+void scratch_overwritten(int device, size_t begin, size_t end) {
+  ScratchTag &tag = scratch_tag(device);
+  if (tag.plan_id != 0 && begin < tag.offset + tag.bytes && tag.offset < end) tag = ScratchTag{};
+}
+
+bool stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Checks of a no-allocation call made before it launches anything (so a rejected call leaves
+// the pages and the array untouched): the array must hold the call's gather rows, plan and
+// partials, and under stream capture the plan must already be in it (a captured copy would
+// only be recorded, not run, and the array would not hold what its tag says).
+nva_status noalloc_prepare(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &d, int num_tokens) {
+  const bool dense = ctx->is_prefill && !ctx->has_tables;
+  size_t gather = 0;
+  if (dense && !d.write_kv) {
+    gather = 2 * (size_t)num_tokens * d.num_kv_heads * d.head_dim * 4 + 16;
+    if (gather > kScratchBytes)
+      return fail(ctx, NVA_E_ARG,
+                  "this call's gathered K/V rows need %zu bytes of device scratch; the "
+                  "no-allocation entry point has %zu",
+                  gather, kScratchBytes);
+  }
   Plan *plan = nullptr;
-  nva_status st = get_plan(ctx, key, &plan);
+  int hpw_row = 0, hpw_tile = 0;
+  nva_status st = attention_plan(ctx, d, dense ? 0 : 1, dense ? 1 : kv->block_size,
+                                 dense ? 0 : kv->num_blocks, num_tokens, &plan, &hpw_row,
+                                 &hpw_tile);
   if (st != NVA_OK) return st;
+  const ScratchLayout l = scratch_layout(gather, *plan, d);
+  if (l.end > kScratchBytes)
+    return fail(ctx, NVA_E_ARG,
+                "this call needs %zu bytes of device scratch (plan %zu, partials %zu, gather "
+                "%zu); the no-allocation entry point has %zu",
+                l.end, plan->host.size(), l.part_bytes, gather, kScratchBytes);
+  const ScratchTag &tag = scratch_tag(ctx->device);
+  if (!plan->host.empty() && (tag.plan_id != plan->id || tag.offset != l.plan_off) &&
+      stream_capturing(ctx->stream))
+    return fail(ctx, NVA_E_ARG,
+                "under stream capture the step's plan must already be in the device scratch "
+                "array: make one call with this configuration outside capture first");
+  return NVA_OK;
+}
+
+// The attention part of Attention.forward once the store (if any) is done.  With scr null the
+// plan and partials use the context's buffers; otherwise the scratch array's regions.
+nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &view,
+                         int num_blocks, const float *q, int num_tokens, float *out,
+                         Scratch *scr) {
+  Plan *plan = nullptr;
+  int hpw_row = 0, hpw_tile = 0;
+  nva_status st = attention_plan(ctx, d, view.paged, view.block_size, num_blocks, num_tokens,
+                                 &plan, &hpw_row, &hpw_tile);
+  if (st != NVA_OK) return st;
+  const int window = d.sliding_window > 0 ? d.sliding_window : 0;
 
   const size_t parts = (size_t)plan->num_parts * d.num_heads;
-  const size_t part_bytes = parts * (2 + (size_t)d.head_dim) * sizeof(float);
   char *pbase = nullptr;
   float *pm = nullptr;
   if (!scr) {
+    const size_t part_bytes = parts * (2 + (size_t)d.head_dim) * sizeof(float);
     st = upload_plan(ctx, plan);
     if (st != NVA_OK) return st;
     pbase = static_cast<char *>(plan->dev.ptr);
     if (parts > 0) HIP_TRY(ctx, ctx->d_part.reserve(part_bytes), "partial buffer");
     pm = static_cast<float *>(ctx->d_part.ptr);
   } else {
-    // Regions after the gather rows: [plan lists | partials], 256-byte aligned.
-    const size_t plan_off = align256(scr->used);
-    const size_t part_off = align256(plan_off + plan->host.size());
-    if (part_off + part_bytes > kScratchBytes)
-      return fail(ctx, NVA_E_ARG,
-                  "this call needs %zu bytes of device scratch (plan %zu, partials %zu, gather "
-                  "%zu); the no-allocation entry point has %zu",
-                  part_off + part_bytes, plan->host.size(), part_bytes, scr->used,
-                  kScratchBytes);
-    pbase = scr->base + plan_off;
-    pm = reinterpret_cast<float *>(scr->base + part_off);
+    // The sizes and the capture rule were checked before anything was launched
+    // (noalloc_prepare); these are the same regions.
+    const ScratchLayout l = scratch_layout(scr->used, *plan, d);
+    pbase = scr->base + l.plan_off;
+    pm = reinterpret_cast<float *>(scr->base + l.part_off);
     // Skip the copy when this device's array already holds this very plan at this offset.
     ScratchTag &tag = scratch_tag(ctx->device);
-    if (!plan->host.empty() && (tag.plan_id != plan->id || tag.offset != plan_off)) {
+    if (!plan->host.empty() && (tag.plan_id != plan->id || tag.offset != l.plan_off)) {
+      tag = ScratchTag{};
       HIP_TRY(ctx, hipMemcpyAsync(pbase, plan->host.data(), plan->host.size(),
                                   hipMemcpyHostToDevice, ctx->stream),
               "plan copy to scratch");
       tag.plan_id = plan->id;
-      tag.offset = plan_off;
+      tag.offset = l.plan_off;
+      tag.bytes = plan->host.size();
     }
+    if (l.part_bytes > 0) scratch_overwritten(ctx->device, l.part_off, l.end);
   }
 
   // "attention" times the whole part below, kernels that overlap counted once.
@@ -875,7 +944,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     t.hq = d.num_heads;
     t.hkv = d.num_kv_heads;
     t.head_dim = d.head_dim;
-    t.window = key.window;
+    t.window = window;
     t.scale = d.scale;
     t.part_m = pm;
     t.part_l = pm + parts;
@@ -1019,13 +1088,10 @@ nva_status attention_after_store(nva_ctx *ctx, nva_kv *kv, const nva_attn_desc &
       HIP_TRY(ctx, ctx->d_gather.reserve(gather_bytes), "gather buffer");
       gk = static_cast<float *>(ctx->d_gather.ptr);
     } else {
-      if (gather_bytes > kScratchBytes)
-        return fail(ctx, NVA_E_ARG,
-                    "this call's gathered K/V rows need %zu bytes of device scratch; the "
-                    "no-allocation entry point has %zu",
-                    gather_bytes, kScratchBytes);
+      // Size checked by noalloc_prepare.  The rows overwrite the front of the array.
       gk = reinterpret_cast<float *>(scr->base);
       scr->used = gather_bytes;
+      scratch_overwritten(ctx->device, 0, gather_bytes);
     }
     float *gv = gk + (size_t)num_tokens * row;
     GatherLaunch g;
@@ -1128,10 +1194,6 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
   }
   ctx->stream = ctx->own_stream;
   ctx->scratch = scratch_address(device, &ctx->scratch_err);
-  if (const char *b = getenv("NVA_LINEAR_BACKEND")) {
-    if (!strcmp(b, "native")) ctx->linear_backend = nva_ctx::kLinearNative;
-    if (!strcmp(b, "vendor")) ctx->linear_backend = nva_ctx::kLinearVendor;
-  }
   *out = ctx;
   return NVA_OK;
 }
@@ -1155,7 +1217,6 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   ctx->d_k_rot.release();
   ctx->d_v_norm.release();
   ctx->d_lin.release();
-  vendor_gemm_destroy(ctx->gemm);
   ctx->d_gather.release();
   (void)hipEventDestroy(ctx->fork_ev);
   (void)hipEventDestroy(ctx->join_ev);
@@ -1544,6 +1605,10 @@ static nva_status attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_des
     return fail(ctx, NVA_E_ARG, "device pointers must be 16-byte aligned");
   const nva_attn_desc d = *desc;
   const int layer = d.kv_layer_index;
+  if (scr) {
+    st = noalloc_prepare(ctx, kv, d, num_tokens);
+    if (st != NVA_OK) return st;
+  }
   // Store first, Attention.java:157-160.
   if (d.write_kv && kv->k[layer] && ctx->has_slots && ctx->num_slots == num_tokens &&
       num_tokens > 0) {
@@ -1732,29 +1797,13 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
   if (!x || !weight || !y) return fail(ctx, NVA_E_ARG, "x, weight and y are required");
   if (in % 4 != 0)
     return fail(ctx, NVA_E_UNSUPPORTED, "linear needs in %% 4 == 0 (got %d)", in);
+  // The kernels address a tile's 128 rows with 32-bit byte offsets.
+  if (in >= (1 << 22))
+    return fail(ctx, NVA_E_UNSUPPORTED, "linear needs in < 4194304 (got %d)", in);
   if (!aligned16(x) || !aligned16(weight))
     return fail(ctx, NVA_E_ARG, "x and weight must be 16-byte aligned device pointers");
   const int cus = std::max(1, ctx->num_cus);
   const int64_t blocks = (int64_t)((out + 31) / 32) * ((rows + 31) / 32);
-  // auto: the library's GEMV and 32 x 32-block kernels while the output fits one block per CU
-  // (decode batches: they beat hipBLASLt's kernel plus its per-call host cost), hipBLASLt for
-  // larger GEMMs, where its stream-K tiles beat the library's 128 x 128 tiles.
-  const bool vendor = ctx->linear_backend == nva_ctx::kLinearVendor ||
-                      (ctx->linear_backend == nva_ctx::kLinearAuto &&
-                       rows > linear_gemv_max_rows() && blocks > cus);
-  if (vendor) {
-    // A plain GEMM: hipBLASLt's fp32 kernels with the bias in their epilogue (vendor_gemm.cpp).
-    std::string e;
-    if (!ctx->gemm) {
-      ctx->gemm = vendor_gemm_create(ctx->device, &e);
-      if (!ctx->gemm) return fail(ctx, NVA_E_HIP, "%s", e.c_str());
-    }
-    Timed tm(ctx, "linear");
-    if (!vendor_gemm_run(ctx->gemm, x, weight, bias, y, rows, in, out, ctx->stream, &e))
-      return fail(ctx, NVA_E_HIP, "%s", e.c_str());
-    tm.done();
-    return NVA_OK;
-  }
   if (rows <= linear_gemv_max_rows()) {
     // A few rows: stream W once (GEMV), no tiles, no K slices.
     LinearLaunch g{};
@@ -1800,22 +1849,23 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
     tm.done();
     return NVA_OK;
   }
-  // K slices: the count s that minimises a per-CU cost model.  A CU runs the K tiles of its
-  // workgroups at about the same rate whether one or two are resident, so the kernel takes
-  // ceil(tiles * s / CUs) workgroup rounds of ceil(K tiles / s) K tiles each (about 2.1 us per
-  // 128 x 128 x 32 K tile); s > 1 adds the partial planes (written, then read by the reduce, at
-  // about 5 TB/s) and the reduce launch.  Every slice keeps at least 4 K tiles.
+  // K slices: the count s that minimises a per-CU cost model.  Two 128 x 64 workgroups share a
+  // CU and run their K tiles together at about 1.8 us per pair of 128 x 64 x 32 tiles, so the
+  // kernel takes ceil(tiles * s / (2 CUs)) rounds of ceil(K tiles / s) K tiles; s > 1 adds the
+  // partial planes (written, then read by the reduce, at about 5 TB/s) and the reduce launch.
+  // Every slice keeps at least 4 K tiles.
   const int64_t tiles = (int64_t)((out + linear_tile_cols() - 1) / linear_tile_cols()) *
                         ((rows + linear_tile_rows() - 1) / linear_tile_rows());
   const int bk = linear_k_tile();
   const int nkt = (in + bk - 1) / bk;
+  const int64_t slots = 2 * (int64_t)cus;
   int splits = 1;
   double best = 0.0;
   for (int sl = 1; sl <= std::max(1, nkt / 4); sl++) {
     const int per = (nkt + sl - 1) / sl;
     if (sl > 1 && (nkt + per - 1) / per != sl) continue;  // same slices as a smaller count
-    const double rounds = (double)((tiles * sl + cus - 1) / cus);
-    double us = rounds * per * 2.1;
+    const double rounds = (double)((tiles * sl + slots - 1) / slots);
+    double us = rounds * per * 1.8;
     if (sl > 1) us += 2.0 * sl * (double)rows * out * 4.0 / 5.0e6 + 3.0;
     if (sl == 1 || us < best) {
       best = us;
@@ -1834,10 +1884,6 @@ nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
   a.k = in;
   a.splits = splits;
   a.k_per_split = kt_per * bk;
-  // A grid of at most one workgroup per CU runs eight-wave workgroups (32 x 64 per wave):
-  // 4096 x 2048 -> 1024 takes 159 us against 165 us with four waves, the 256-row decode batch
-  // 27.5 against 31 us; larger grids keep four waves (2112 x 4096 -> 2560: 377 vs 371 us).
-  a.waves_m = tiles * splits <= cus ? 4 : 2;
   if (splits > 1) {
     HIP_TRY(ctx, ctx->d_lin.reserve((size_t)splits * rows * out * sizeof(float)),
             "linear partial buffer");

@@ -11,19 +11,27 @@
 //   * skinny_kernel when the 32 x 32 blocks of y number at most one per CU (decode batches of
 //     tens to a few hundred rows): one block per workgroup, K split over its eight waves, each
 //     streaming its own K range through a private LDS ring (below);
-//   * linear_kernel otherwise.  A workgroup owns a 128 x 128 tile of y and one K slice: four
-//     waves of 64 x 64 (2 x 2 blocks of v_mfma_f32_32x32x2_f32), or, when the grid has no more
-//     workgroups than CUs, eight waves of 32 x 64, so each SIMD still has two waves to switch
-//     between.
+//   * linear_kernel otherwise.  A workgroup owns a 128 x 64 tile of y and one K slice; its four
+//     waves own 32 rows x 64 columns each (2 blocks of v_mfma_f32_32x32x2_f32).  Two workgroups
+//     share a CU (48 KB of LDS, 88 VGPRs each), so while one waits at its barrier the other's
+//     MFMAs run on every SIMD: with one 128 x 128 workgroup of eight waves per CU, both waves of
+//     a SIMD stopped at the same barrier every tile (28% of wave cycles waiting, MFMA busy 0.77,
+//     against 0.93 of the fp32 peak here on large GEMMs).
 //   * x and W are both K-contiguous, so the A operand (x rows) and the B operand (W rows) are
-//     read the same way: for each 8-wide K chunk a lane (i, h) reads one float4 of its row
-//     (elements 4h .. 4h + 3), which feeds 4 MFMA steps -- step s contracts k = 4h + s, a
-//     permutation of the chunk that A and B share.
-//   * K tiles of 32 are copied HBM -> LDS with 16-byte loads that write LDS directly (buffer
-//     loads from a uniform descriptor for interior tiles), double-buffered, one barrier per
-//     tile; each 128-byte row of a tile has its 16-byte chunks XOR-swizzled by ((row >> 1) & 7):
-//     measured free of LDS bank conflicts (row & 7: half of the LDS-active cycles were conflict
-//     stalls).
+//     read the same way: for each 8-wide K step a lane (i, h) reads one float4 of its row
+//     (elements 4h .. 4h + 3 of the step), which feeds 4 MFMAs -- MFMA s contracts
+//     k = {s, 4 + s} of the step, a permutation that A and B share.
+//   * K tiles of 32 are copied HBM -> LDS with buffer loads that write LDS directly, from a
+//     wave-uniform base (row m0 / n0, column kt) plus fixed 32-bit lane offsets (rows past the
+//     matrix edge repeat its last row; their sums are never stored).  Each 128-byte row of a
+//     tile has its 16-byte chunks XOR-swizzled by ((row >> 1) & 7): measured free of LDS bank
+//     conflicts.  The copies are issued through copy16_to_lds_async, so the compiler adds no wait
+//     on them before the LDS reads of another stage.
+//   * Double-buffered, one barrier per K tile, placed before the tile's last 8-k step: the last
+//     step's fragments are already in registers, so the barrier (every wave has read this
+//     stage, and the next tile has landed) is followed at once by the next tile's copies into
+//     this stage and by MFMAs.  The next step's fragments are read while the current step's 8
+//     MFMAs run.
 //   * Output block layout (32 x 32, 16 values per lane): value r of lane (i, h) is row
 //     8 * (r / 4) + 4 * h + r % 4, column i -- lanes 0..31 write 128 contiguous bytes.
 //   * When the grid alone cannot fill the chip, K is split over blockIdx.z (both MFMA
@@ -41,180 +49,174 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int BM = 128, BN = 64, BK = 32;  // linear_kernel tile
 constexpr int kSkinnyWaves = 8;  // waves of a skinny_kernel workgroup (two per SIMD)
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
-typedef float f4v __attribute__((ext_vector_type(4)));
-
-// ds_read_b128 the compiler does not see as an LDS read, so it adds no wait for every
-// outstanding LDS copy before it (it cannot tell a ring's stages apart); the caller waits
-// (lgkmcnt) before using the value, tying the wait to the registers.
-__device__ __forceinline__ f4v lds_read4(const float *p) {
-  const unsigned addr = (unsigned)(size_t)(const __attribute__((address_space(3))) float *)p;
-  f4v v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
-
-// Wait until at most N vector memory operations are outstanding.
-template <int N> __device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
+template <int N> struct IntC { static constexpr int value = N; };
+template <bool B> struct BoolC { static constexpr bool value = B; };
 
 }  // namespace
 
-// WM x 2 waves; wave (wm, wn) owns 128/WM rows x 64 columns of the tile as MB x 2 blocks of
-// 32 x 32.  WM = 2: four waves of 64 x 64 (64 accumulators), two workgroups per CU; WM = 4:
-// eight waves of 32 x 64 (32 accumulators), two workgroups per CU and four waves per SIMD.
-template <int WM>
-__global__ void __launch_bounds__(64 * WM * 2) __attribute__((amdgpu_waves_per_eu(WM == 4 ? 4 : 2)))
-linear_kernel(LinearLaunch a) {
-  constexpr int NW = WM * 2;       // waves
-  constexpr int MB = BM / WM / 32; // 32-row blocks per wave
-  constexpr int LPW = 16 / NW;     // tile-copy instructions per wave per operand
-  // Two buffers of the A (x) and B (W) tiles, as separate arrays so the compiler sees that the
-  // copies into one never alias the reads of the other.
-  __shared__ __attribute__((aligned(16))) float sa0[BM * BK];
-  __shared__ __attribute__((aligned(16))) float sb0[BN * BK];
-  __shared__ __attribute__((aligned(16))) float sa1[BM * BK];
-  __shared__ __attribute__((aligned(16))) float sb1[BN * BK];
+// One 128 x 64 tile of y (or of a K slice's partial plane) per workgroup; wave w owns rows
+// 32 w .. 32 w + 31 as two 32 x 32 blocks.
+__global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
+  constexpr int LA = BM / 32, LB = BN / 32;  // copy instructions per wave per tile (8 rows each)
+  constexpr int OPS = LA + LB;
+  constexpr int STAGE = (BM + BN) * BK;      // floats: A rows, then B rows
+  __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
 
   const int n0 = blockIdx.x * BN;
   const int m0 = blockIdx.y * BM;
   const int kb = blockIdx.z * a.k_per_split;
   const int ke = min(a.k, kb + a.k_per_split);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
-  const int lane = threadIdx.x & 63;
-  const int wm = wave >> 1, wn = wave & 1;  // wave = 2 * wm + wn
-  const int i = lane & 31;  // MFMA row (A) / column (B) index of this lane
-  const int h = lane >> 5;  // which half of an 8-wide K chunk this lane supplies
-
-  f32x16 acc[MB][2];
-#pragma unroll
-  for (int bm = 0; bm < MB; bm++)
-#pragma unroll
-    for (int bn = 0; bn < 2; bn++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[bm][bn][r] = 0.0f;
-
-  // Copy instruction p of wave w moves rows [8g, 8g + 8) of a tile, g = 4p + w: lane l takes
-  // row 8g + l / 8, LDS chunk position l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7).
-  const int lrow = lane >> 3;
-  const int lpos = lane & 7;
-  // An interior tile (all 128 rows of x and of W exist, and the K tile lies inside the slice)
-  // is copied from a wave-uniform base at (row m0 or n0, column kt) plus these fixed byte
-  // offsets, through buffer descriptors: no per-lane address arithmetic.
-  // (Offsets and the descriptor size are 32-bit: 128 rows of k floats must stay below 2 GiB.)
-  const bool interior = m0 + BM <= a.m && n0 + BN <= a.n && a.k < (1 << 22);
-  uint32_t loff[LPW];
-#pragma unroll
-  for (int p = 0; p < LPW; p++) {
-    const int r = 8 * (NW * p + wave) + lrow;
-    loff[p] = (uint32_t)r * (uint32_t)a.k * 4u + (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
-  }
-  const int span_bytes = ((BM - 1) * a.k + BK) * 4;  // rows m0.. (n0..), columns kt..kt+BK-1
-  auto issue = [&](int kt, float *da, float *db) {
-    if (interior && kt + BK <= ke) {
-      const float *xb = a.x + (size_t)m0 * a.k + kt;
-      const float *wb = a.w + (size_t)n0 * a.k + kt;
-#pragma unroll
-      for (int p = 0; p < LPW; p++) {
-        const int g = NW * p + wave;
-        copy16_to_lds(xb, span_bytes, loff[p], da + g * 8 * BK);
-        copy16_to_lds(wb, span_bytes, loff[p], db + g * 8 * BK);
-      }
-      return;
-    }
-#pragma unroll
-    for (int p = 0; p < LPW; p++) {
-      const int g = NW * p + wave;
-      const int r = 8 * g + lrow;
-      int kc = kt + 4 * (lpos ^ ((r >> 1) & 7));
-      kc = kc < ke ? kc : kb;  // past the slice: a valid address, zeroed at use
-      const int xr = min(m0 + r, a.m - 1);
-      const int wr = min(n0 + r, a.n - 1);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void *)(a.x + (size_t)xr * a.k + kc),
-          (__attribute__((address_space(3))) void *)(da + g * 8 * BK), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void *)(a.w + (size_t)wr * a.k + kc),
-          (__attribute__((address_space(3))) void *)(db + g * 8 * BK), 16, 0, 0);
-    }
-  };
-
-  // full: every chunk of the tile lies inside the slice (all but a ragged last tile); the
-  // chunks of a ragged tile past the slice end are zeroed.
-  auto compute = [&](int kt, const float *sa, const float *sb, bool full) {
-#pragma unroll
-    for (int kk = 0; kk < BK / 8; kk++) {
-      const int c = 2 * kk + h;  // this lane's 16-byte chunk of the row
-      float4 av[MB], bv[2];
-#pragma unroll
-      for (int b = 0; b < MB; b++) {
-        const int ra = wm * 32 * MB + b * 32 + i;
-        av[b] = ld4(sa + ra * BK + 4 * (c ^ ((ra >> 1) & 7)));
-      }
-#pragma unroll
-      for (int b = 0; b < 2; b++) {
-        const int rb = wn * 64 + b * 32 + i;
-        bv[b] = ld4(sb + rb * BK + 4 * (c ^ ((rb >> 1) & 7)));
-      }
-      if (!full && !(kt + 4 * c < ke)) {
-#pragma unroll
-        for (int b = 0; b < MB; b++) av[b] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int b = 0; b < 2; b++) bv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int bm = 0; bm < MB; bm++)
-#pragma unroll
-        for (int bn = 0; bn < 2; bn++) {
-          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].x, bv[bn].x, acc[bm][bn], 0, 0, 0);
-          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].y, bv[bn].y, acc[bm][bn], 0, 0, 0);
-          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].z, bv[bn].z, acc[bm][bn], 0, 0, 0);
-          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bm].w, bv[bn].w, acc[bm][bn], 0, 0, 0);
-        }
-    }
-  };
-
-  // Double-buffered K loop with one barrier per tile: at the barrier of tile t every wave has
-  // finished tile t-1, whose buffer is then refilled with tile t+1.
   const int ntiles = (ke - kb + BK - 1) / BK;
-  if (ntiles > 0) issue(kb, sa0, sb0);
-  for (int t = 0; t < ntiles; t += 2) {
-    const int kt = kb + t * BK;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies of tile t landed
-    __syncthreads();
-    if (t + 1 < ntiles) issue(kt + BK, sa1, sb1);
-    compute(kt, sa0, sb0, kt + BK <= ke);
-    // A conditional block rather than a mid-loop exit, so the accumulators leave the loop
-    // from one place and keep one set of registers.
-    if (t + 1 < ntiles) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (t + 2 < ntiles) issue(kt + 2 * BK, sa0, sb0);
-      compute(kt + BK, sa1, sb1, kt + 2 * BK <= ke);
+  const bool ragged = (ke - kb) % BK != 0;  // the last tile ends inside a K tile
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 31;  // MFMA row (A) / column (B) index of this lane
+  const int h = lane >> 5;  // which float4 of an 8-wide K step this lane supplies
+
+  f32x16 acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    acc0[r] = 0.0f;
+    acc1[r] = 0.0f;
+  }
+
+  // Copy instruction p of wave w moves rows [8g, 8g + 8), g = 4p + w, of A (p < LA) or of B:
+  // lane l takes row 8g + l / 8 at LDS chunk position l % 8, i.e. global chunk
+  // (l % 8) ^ ((row >> 1) & 7).  Offsets are 32-bit: 128 rows of k floats stay below 2 GiB.
+  const int lrow = lane >> 3, lpos = lane & 7;
+  const int rows_a = min(BM, a.m - m0), rows_b = min(BN, a.n - n0);
+  uint32_t off[OPS];
+#pragma unroll
+  for (int p = 0; p < OPS; p++) {
+    const int r = 8 * (4 * (p < LA ? p : p - LA) + wave) + lrow;
+    const int rows = p < LA ? rows_a : rows_b;
+    off[p] = (uint32_t)min(r, rows - 1) * (uint32_t)a.k * 4u +
+             (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+  }
+  const uint32_t lds0 = lds_address(lds);
+  auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+    // The descriptors end at the last row's column min(kt + BK, k): nothing past the matrix.
+    const int cols = min(BK, a.k - kt);
+    const float *xb = a.x + (size_t)m0 * a.k + kt;
+    const float *wb = a.w + (size_t)n0 * a.k + kt;
+    const uint32_t dst = lds0 + (uint32_t)(stage * STAGE) * 4u;
+#pragma unroll
+    for (int p = 0; p < LA; p++)
+      copy16_to_lds_async(xb, ((rows_a - 1) * a.k + cols) * 4, off[p],
+                          dst + (uint32_t)((4 * p + wave) * 8 * BK) * 4u);
+#pragma unroll
+    for (int p = 0; p < LB; p++)
+      copy16_to_lds_async(wb, ((rows_b - 1) * a.k + cols) * 4, off[LA + p],
+                          dst + (uint32_t)((BM + (4 * p + wave) * 8) * BK) * 4u);
+  };
+
+  // Fragments of 8-k step kk of a stage: A rows 32 w + i, B rows i and 32 + i, chunk 2 kk + h.
+  const int ra = 32 * wave + i;
+  const int xa = 4 * ((ra >> 1) & 7), xb = 4 * ((i >> 1) & 7);  // chunk swizzles (B: same for i, 32 + i)
+  auto frag = [&](int stage, int kk, float4 &av, float4 &b0, float4 &b1) __attribute__((always_inline)) {
+    const float *s = lds + stage * STAGE;
+    const int c = 4 * (2 * kk + h);
+    av = ld4(s + ra * BK + (c ^ xa));
+    b0 = ld4(s + (BM + i) * BK + (c ^ xb));
+    b1 = ld4(s + (BM + 32 + i) * BK + (c ^ xb));
+  };
+  // Chunks of a ragged last tile past the slice end are zero in both operands.
+  auto mask = [&](int kt, int kk, float4 &av, float4 &b0, float4 &b1) __attribute__((always_inline)) {
+    if (kt + 4 * (2 * kk + h) >= ke) {
+      av = make_float4(0.f, 0.f, 0.f, 0.f);
+      b0 = av;
+      b1 = av;
     }
+  };
+  // The two blocks' accumulations alternate, so no MFMA waits on the one before it.
+  auto mma = [&](const float4 &av, const float4 &b0, const float4 &b1) __attribute__((always_inline)) {
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b0.x, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, b1.x, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b0.y, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, b1.y, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b0.z, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, b1.z, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b0.w, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, b1.w, acc1, 0, 0, 0);
+  };
+
+  float4 fa0, fb00, fb01, fa1, fb10, fb11;  // two fragment sets: steps 0/2 and 1/3
+  if (ntiles > 0) {
+    issue(kb, 0);
+    if (ntiles > 1) {
+      issue(kb + BK, 1);
+      wait_copies<OPS>();
+    } else {
+      wait_copies<0>();
+    }
+    lds_barrier();
+    frag(0, 0, fa0, fb00, fb01);
+  }
+  // Tile t in stage s (a constant: two tiles per loop iteration).  RAGGED (the last tile of a
+  // slice that ends inside it) zeroes the chunks past the slice end; it is a separate copy of
+  // the body, so the common body is straight-line code the compiler can interleave.
+  auto tile = [&](int t, auto s_, auto ragged_) __attribute__((always_inline)) {
+    constexpr int s = decltype(s_)::value;
+    constexpr bool RAGGED = decltype(ragged_)::value;
+    const int kt = kb + t * BK;
+    frag(s, 1, fa1, fb10, fb11);
+    if (RAGGED) mask(kt, 0, fa0, fb00, fb01);
+    mma(fa0, fb00, fb01);
+    frag(s, 2, fa0, fb00, fb01);
+    if (RAGGED) mask(kt, 1, fa1, fb10, fb11);
+    mma(fa1, fb10, fb11);
+    frag(s, 3, fa1, fb10, fb11);
+    if (RAGGED) mask(kt, 2, fa0, fb00, fb01);
+    mma(fa0, fb00, fb01);
+    if (t + 1 < ntiles) {
+      // This wave's reads of stage s have returned (step 3 is in registers) and its copies of
+      // tile t + 1 have landed (tile t + 2's are not issued yet); after the barrier the same
+      // holds for every wave, so stage s takes tile t + 2 and tile t + 1 is read.
+      wait_lds_reads();
+      wait_copies<0>();
+      lds_barrier();
+      if (t + 2 < ntiles) issue(kt + 2 * BK, s);
+      frag(s ^ 1, 0, fa0, fb00, fb01);
+    }
+    if (RAGGED) mask(kt, 3, fa1, fb10, fb11);
+    mma(fa1, fb10, fb11);
+  };
+  const int full_tiles = ragged ? ntiles - 1 : ntiles;
+  int t = 0;
+  for (; t + 1 < full_tiles; t += 2) {
+    tile(t, IntC<0>{}, BoolC<false>{});
+    tile(t + 1, IntC<1>{}, BoolC<false>{});
+  }
+  if (t < full_tiles) {
+    tile(t, IntC<0>{}, BoolC<false>{});
+    t++;
+  }
+  if (t < ntiles) {  // the ragged last tile, in stage t % 2
+    if (t & 1)
+      tile(t, IntC<1>{}, BoolC<true>{});
+    else
+      tile(t, IntC<0>{}, BoolC<true>{});
   }
 
   const bool direct = a.splits == 1;
   float *dst = direct ? a.y : a.part + (size_t)blockIdx.z * a.m * a.n;
 #pragma unroll
-  for (int bm = 0; bm < MB; bm++)
+  for (int bn = 0; bn < 2; bn++) {
+    const int col = n0 + bn * 32 + i;
+    if (col >= a.n) continue;
+    const float bias = direct && a.bias ? a.bias[col] : 0.0f;
+    const f32x16 &acc = bn == 0 ? acc0 : acc1;
 #pragma unroll
-    for (int bn = 0; bn < 2; bn++) {
-      const int col = n0 + wn * 64 + bn * 32 + i;
-      if (col >= a.n) continue;
-      const float bias = direct && a.bias ? a.bias[col] : 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * 32 * MB + bm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row < a.m) dst[(size_t)row * a.n + col] = acc[bm][bn][r] + bias;
-      }
+    for (int r = 0; r < 16; r++) {
+      const int row = m0 + 32 * wave + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (row < a.m) dst[(size_t)row * a.n + col] = acc[r] + bias;
     }
+  }
 }
 
 // y = bias + sum over slices of the partials, slices added in order; four outputs per thread
@@ -252,13 +254,14 @@ __global__ void __launch_bounds__(256) linear_reduce_kernel(LinearLaunch a) {
   }
 }
 
+
 // Tens to a few hundred rows (decode batches): one 32 x 32 block of y per workgroup, so the
 // 256-row, 1024-column o_proj alone has 256 workgroups, and the K slice split over the
 // workgroup's NW waves.  No operand is shared between the waves, so each wave streams its own
 // K range through a private ring of PF LDS stages (32 x rows and 32 W rows of 32 k each),
-// copied with global_load_lds_dwordx4 so that every copy instruction reads whole 128-byte
-// rows, with the chunk swizzle of the tiled kernel; no barrier until the end.  A stage is read
-// into registers whole, its refill issued, then its 16 MFMAs run: lane (i, h) holds
+// copied with buffer loads that write LDS directly so that every copy instruction reads whole
+// 128-byte rows, with the tiled kernel's chunk swizzle; no barrier until the end.  A stage is
+// read into registers whole, its refill issued, then its 16 MFMAs run: lane (i, h) holds
 // k = kt + 16h .. kt + 16h + 15 of row i as four float4, and MFMA step j contracts
 // k = kt + 16h + j (the same permutation for A and B).  The waves' blocks meet in LDS and are
 // added in wave order (plus the bias, or into the slice's partial plane).  Eight waves with two
@@ -268,6 +271,7 @@ template <int NW, int PF>
 __global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
   constexpr int KI = 32;       // k per stage
   constexpr int ST = 32 * KI;  // floats per operand per stage
+  constexpr int OPS = 8;       // copy instructions per stage
   __shared__ __attribute__((aligned(16))) float ring[NW][PF][2][ST];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -279,50 +283,34 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
   const int wk0 = kb + w * per, wk1 = min(ke, wk0 + per);
   const int iters = wk1 > wk0 ? (wk1 - wk0 + KI - 1) / KI : 0;
 
-  // Copy instruction g moves rows [8g, 8g + 8) of a stage: lane l takes row 8g + l / 8, LDS
-  // chunk position l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7).  Rows and columns past
-  // the edge copy the last valid row (their sums are not stored); chunks past the wave's K
-  // range copy a valid address and are zeroed at use.
+  // Copy instruction g moves rows [8g, 8g + 8) of a stage: lane l takes row 8g + l / 8 (rows
+  // past the edge repeat the last valid row; their sums are not stored), LDS chunk position
+  // l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7), from wave-uniform bases (row m0 / n0,
+  // column kt).  Chunks past the wave's K range are zeroed at use.
   const int lrow = lane >> 3, lpos = lane & 7;
-  // A full block (32 rows of x and of W) and a stage inside the wave's K range: copied from
-  // wave-uniform bases (row m0 / n0, column kt) plus fixed byte offsets, shared by x and W
-  // (both K-contiguous with row stride k), through buffer descriptors.
-  const bool full_block = m0 + 32 <= a.m && n0 + 32 <= a.n && a.k < (1 << 22);
-  uint32_t soff[4];
+  const int rows_x = min(32, a.m - m0), rows_w = min(32, a.n - n0);
+  uint32_t offx[4], offw[4];
 #pragma unroll
   for (int g = 0; g < 4; g++) {
     const int r = 8 * g + lrow;
-    soff[g] = (uint32_t)r * (uint32_t)a.k * 4u + (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+    const uint32_t c = (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+    offx[g] = (uint32_t)min(r, rows_x - 1) * (uint32_t)a.k * 4u + c;
+    offw[g] = (uint32_t)min(r, rows_w - 1) * (uint32_t)a.k * 4u + c;
   }
-  const int span_bytes = (31 * a.k + KI) * 4;
-  auto issue = [&](int it, int st) {
+  const uint32_t ring0 = lds_address(&ring[w][0][0][0]);
+  auto issue = [&](int it, int st) __attribute__((always_inline)) {
     const int kt = wk0 + it * KI;
-    if (full_block && kt + KI <= wk1) {
-      const float *xb = a.x + (size_t)m0 * a.k + kt;
-      const float *wb = a.w + (size_t)n0 * a.k + kt;
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        copy16_to_lds(xb, span_bytes, soff[g], &ring[w][st][0][g * 8 * KI]);
-        copy16_to_lds(wb, span_bytes, soff[g], &ring[w][st][1][g * 8 * KI]);
-      }
-      return;
-    }
+    const int cols = min(KI, a.k - kt);  // the descriptors end inside the matrix
+    const float *xb = a.x + (size_t)m0 * a.k + kt;
+    const float *wb = a.w + (size_t)n0 * a.k + kt;
+    const uint32_t dst = ring0 + (uint32_t)(st * 2 * ST) * 4u;
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-      const int r = 8 * g + lrow;
-      int kc = kt + 4 * (lpos ^ ((r >> 1) & 7));
-      kc = kc < wk1 ? kc : 0;
-      const int xr = min(m0 + r, a.m - 1);
-      const int wr = min(n0 + r, a.n - 1);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void *)(a.x + (size_t)xr * a.k + kc),
-          (__attribute__((address_space(3))) void *)(&ring[w][st][0][g * 8 * KI]), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void *)(a.w + (size_t)wr * a.k + kc),
-          (__attribute__((address_space(3))) void *)(&ring[w][st][1][g * 8 * KI]), 16, 0, 0);
+      copy16_to_lds_async(xb, ((rows_x - 1) * a.k + cols) * 4, offx[g], dst + g * 8 * KI * 4);
+      copy16_to_lds_async(wb, ((rows_w - 1) * a.k + cols) * 4, offw[g],
+                          dst + (ST + g * 8 * KI) * 4);
     }
   };
-  constexpr int OPS = 8;  // copy instructions per stage
   f32x16 acc0, acc1;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
@@ -336,42 +324,43 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
 #pragma unroll
     for (int p = 0; p < PF; p++) {
       if (it + p < iters) {
-        // Stage p landed: every later stage issued so far (OPS operations each) may still be in
+        // Stage p landed: every later stage issued so far (OPS copies each) may still be in
         // flight.
         if (it + p + PF - 1 < iters)
-          wait_vm<OPS * (PF - 1)>();
+          wait_copies<OPS * (PF - 1)>();
         else
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          wait_copies<0>();
         const int kt = wk0 + (it + p) * KI;
         const float *sa = ring[w][p][0], *sb = ring[w][p][1];
         const int sw = i * KI, sx = (i >> 1) & 7;
         // The whole stage goes to registers first, so its refill is issued before the MFMAs.
-        f4v av[4], bv[4];
+        float4 av[4], bv[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          av[q] = lds_read4(sa + sw + 4 * ((4 * h + q) ^ sx));
-          bv[q] = lds_read4(sb + sw + 4 * ((4 * h + q) ^ sx));
+          av[q] = ld4(sa + sw + 4 * ((4 * h + q) ^ sx));
+          bv[q] = ld4(sb + sw + 4 * ((4 * h + q) ^ sx));
         }
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]),
-                       "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3])::"memory");
-        if (it + p + PF < iters) issue(it + p + PF, p);
+        if (it + p + PF < iters) {
+          wait_lds_reads();  // the refill overwrites this stage
+          issue(it + p + PF, p);
+        }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           if (kt + 4 * (4 * h + q) >= wk1) {
-            av[q] = f4v{0.f, 0.f, 0.f, 0.f};
-            bv[q] = f4v{0.f, 0.f, 0.f, 0.f};
+            av[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            bv[q] = av[q];
           }
-          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][0], bv[q][0], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][1], bv[q][1], acc1, 0, 0, 0);
-          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][2], bv[q][2], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][3], bv[q][3], acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q].x, bv[q].x, acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q].y, bv[q].y, acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q].z, bv[q].z, acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q].w, bv[q].w, acc1, 0, 0, 0);
         }
       }
     }
   }
   // The wave's block goes to its own first stage (its copies have all landed and been read).
   // Value r of lane (i, h): row 8 * (r / 4) + 4 * h + r % 4, column i.
+  wait_lds_reads();
   float *red = ring[w][0][0];
 #pragma unroll
   for (int r = 0; r < 16; r++) red[(8 * (r >> 2) + 4 * h + (r & 3)) * 32 + i] = acc0[r] + acc1[r];
@@ -516,10 +505,7 @@ hipError_t launch_reduce(const LinearLaunch &a, hipStream_t s) {
 hipError_t launch_linear(const LinearLaunch &a, hipStream_t s) {
   if (a.m <= 0 || a.n <= 0) return hipSuccess;
   const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM, a.splits);
-  if (a.waves_m == 4)
-    hipLaunchKernelGGL(linear_kernel<4>, grid, dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL(linear_kernel<2>, grid, dim3(256), 0, s, a);
+  hipLaunchKernelGGL(linear_kernel, grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   return launch_reduce(a, s);

@@ -137,7 +137,6 @@ struct LinearLaunch {
   float *part;  // [splits, m, n] partial sums when splits > 1
   int32_t m, n, k;
   int32_t splits, k_per_split;
-  int32_t waves_m;  // waves along the tile's rows: 2 (four 64 x 64 waves) or 4 (eight 32 x 64)
 };
 
 struct GatherLaunch {
@@ -162,13 +161,6 @@ hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s);
 // waves; runs the reduce when splits > 1.
 hipError_t launch_skinny(const LinearLaunch &a, hipStream_t s);
 
-// hipBLASLt for o_proj batches (vendor_gemm.cpp): one per context, created on first use.
-struct VendorGemm;
-VendorGemm *vendor_gemm_create(int device, std::string *err);
-void vendor_gemm_destroy(VendorGemm *v);
-// y[rows, out] = x[rows, in] w[out, in]^T (+ bias[out]) on stream; false with *err set on failure.
-bool vendor_gemm_run(VendorGemm *v, const float *x, const float *w, const float *bias, float *y,
-                     int rows, int in, int out, hipStream_t stream, std::string *err);
 int linear_skinny_waves();
 int linear_gemv_max_rows();
 int linear_tile_rows();

@@ -409,9 +409,8 @@ class RMSNorm:
 
 class Linear:
     """Linear.Row(weight [out, in], bias) (layers/Linear.java:296-335): ``forward(x, ctx)`` is
-    Ops.linear, y = x W^T + b, in fp32: the library's GEMV and block kernels for decode batches,
-    hipBLASLt for larger GEMMs (the context's NVA_LINEAR_BACKEND, read at creation, can force
-    either).  ``weight``/``bias`` are
+    Ops.linear, y = x W^T + b, in fp32 on the library's kernels: a GEMV for a few rows, 32 x 32
+    blocks for decode batches, 128 x 64 tiles for larger GEMMs.  ``weight``/``bias`` are
     float32 device tensors kept resident, as the model's weights are."""
 
     def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):

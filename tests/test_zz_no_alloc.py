@@ -171,3 +171,91 @@ def test_rejects_more_than_the_scratch_holds(ctx):
     finally:
         ctx.clear()
         arena.close()
+
+
+def test_plan_reuse_in_one_step_alternating_configurations():
+    """One context and one step, two attention configurations with different plans at the same
+    offset of the array (no window, and a 512-token window): A, A, B, A, B, B.  The repeated
+    calls take the branch that skips the plan copy; every call matches nva_attention_forward bit
+    for bit (a stale plan left in the array would not)."""
+    case = decode_case(64, 39)
+    wl = case.wl
+    with Context(0) as ctx:
+        arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+        arena.write(0, 0, case.k_cache)
+        arena.write(0, 1, case.v_cache)
+        try:
+            ctx.set(**wl.meta.context_args())
+            ctx.bind_kv_cache(arena)
+            q = dev(case.q)
+            layers = {"A": Attention(wl.hq, wl.d, wl.scale, wl.hkv, 0, 0, write_kv=False),
+                      "B": Attention(wl.hq, wl.d, wl.scale, wl.hkv, 512, 0, write_kv=False)}
+            want = {n: a.forward(q, None, None, ctx).cpu().numpy() for n, a in layers.items()}
+            assert not np.array_equal(want["A"], want["B"])
+            for n in "AABABB":
+                out = torch.full((wl.tokens, wl.hq, wl.d), float("nan"), device="cuda")
+                st = noalloc(ctx, arena, layers[n], q, None, None, out)
+                assert st == N.NVA_OK, N.load().nva_last_error(ctx.handle).decode()
+                got = out.cpu().numpy()
+                say(f"no-alloc alternating {n}: max |got - want| = "
+                    f"{float(np.nanmax(np.abs(got - want[n]))):.3e}")
+                assert np.array_equal(bits(got), bits(want[n])), f"call {n} differs"
+        finally:
+            ctx.clear()
+            arena.close()
+
+
+def test_capture_needs_the_plan_in_the_array():
+    """Under stream capture, a call whose plan is not in the array fails before it records
+    anything (the replayed graph leaves the pages untouched); after one eager call the same call
+    captures, and its replay matches nva_attention_forward bit for bit."""
+    case = decode_case(48, 40)
+    wl = case.wl
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s), Context(0, stream=s) as ctx:
+        arena = KvCacheArena(ctx, 1, wl.num_blocks, wl.block_size, wl.hkv, wl.d)
+        arena.write(0, 0, case.k_cache)
+        arena.write(0, 1, case.v_cache)
+        try:
+            ctx.set(**wl.meta.context_args())
+            ctx.bind_kv_cache(arena)
+            attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, 0, 0, write_kv=True)
+            q, k, v = dev(case.q), dev(case.k), dev(case.v)
+            out = torch.full((wl.tokens, wl.hq, wl.d), float("nan"), device="cuda")
+            # Another configuration's plan goes into the array first.
+            other = Attention(wl.hq, wl.d, wl.scale, wl.hkv, 300, 0, write_kv=False)
+            junk = torch.empty_like(out)
+            assert noalloc(ctx, arena, other, q, None, None, junk) == N.NVA_OK
+            s.synchronize()
+            k_before = arena.get_key_cache(0).copy()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                junk.mul_(1.0)  # keeps the graph non-empty
+                st = noalloc(ctx, arena, attn, q, k, v, out)
+            msg = N.load().nva_last_error(ctx.handle).decode()
+            say(f"no-alloc capture with a stale plan: status {st}: {msg}")
+            assert st == N.NVA_E_ARG and "capture" in msg
+            g.replay()
+            s.synchronize()
+            assert np.array_equal(bits(arena.get_key_cache(0)), bits(k_before)), \
+                "the rejected call recorded the store"
+            # One eager call puts the plan in the array; then capture works.
+            assert noalloc(ctx, arena, attn, q, k, v, out) == N.NVA_OK
+            s.synchronize()
+            want = attn.forward(q, k, v, ctx).cpu().numpy()
+            g2 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g2, stream=s):
+                st = noalloc(ctx, arena, attn, q, k, v, out)
+            assert st == N.NVA_OK, N.load().nva_last_error(ctx.handle).decode()
+            for r in range(2):
+                out.fill_(float("nan"))
+                s.synchronize()
+                g2.replay()
+                s.synchronize()
+                got = out.cpu().numpy()
+                say(f"no-alloc capture replay {r}: max |got - want| = "
+                    f"{float(np.nanmax(np.abs(got - want))):.3e}")
+                assert np.array_equal(bits(got), bits(want)), f"replay {r} differs"
+        finally:
+            ctx.clear()
+            arena.close()
