@@ -114,6 +114,18 @@ nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block
                          nva_kv **out);
 /* KvCacheArena.close(), KvCacheArena.java:130-134: frees the device pages. */
 nva_status nva_kv_destroy(nva_kv *kv);
+/* The heap cap of Config.resolveNumKvcacheBlocks (llm/Config.java:93-125) with the device's free
+ * HBM (hipMemGetInfo on the context's device, at the call) in place of
+ * Runtime.getRuntime().maxMemory(): *blocks = max(32, floor(free * fraction / bytes_per_block)),
+ * capped at INT32_MAX, where bytes_per_block = 2 * block_size * num_kv_heads * head_dims[l] * 4
+ * summed over the layers that get pages (allocate == NULL: every layer; the reference skips
+ * shared-KV layers the same way).  A query only: nothing is allocated.  The caller takes
+ * min(estimated, *blocks) exactly as the reference does with its heap cap, then passes the
+ * result to nva_kv_create.  fraction must be in (0, 1] (kvHeapFraction's range, Config.java:66-69);
+ * *free_bytes (may be NULL) receives the free HBM the cap was computed from. */
+nva_status nva_kv_blocks_that_fit(nva_ctx *ctx, int num_layers, int block_size, int num_kv_heads,
+                                  const int32_t *head_dims, const uint8_t *allocate,
+                                  float fraction, int *blocks, int64_t *free_bytes);
 /* getKeyCache/getValueCache(layer), KvCacheArena.java:111-124: device pointers and the byte
  * size of each buffer (0 and NULL for an unallocated layer).  NVA_E_LAYER if out of range. */
 nva_status nva_kv_layer(nva_kv *kv, int layer, void **key, void **value, int64_t *bytes);

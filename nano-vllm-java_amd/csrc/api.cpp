@@ -1310,6 +1310,7 @@ nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block
     if (e == hipSuccess) e = hipMemsetAsync(pk, 0, bytes, ctx->stream);
     if (e == hipSuccess) e = hipMemsetAsync(pv, 0, bytes, ctx->stream);
     if (e != hipSuccess) {
+      (void)hipGetLastError();  // a failed allocation must not surface at a later launch check
       if (pk) (void)hipFree(pk);
       if (pv) (void)hipFree(pv);
       nva_kv_destroy(kv);
@@ -1321,6 +1322,34 @@ nva_status nva_kv_create(nva_ctx *ctx, int num_layers, int num_blocks, int block
   }
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "KV arena zero-fill");
   *out = kv;
+  return NVA_OK;
+}
+
+nva_status nva_kv_blocks_that_fit(nva_ctx *ctx, int num_layers, int block_size, int num_kv_heads,
+                                  const int32_t *head_dims, const uint8_t *allocate,
+                                  float fraction, int *blocks, int64_t *free_bytes) {
+  if (!ctx || !blocks) return NVA_E_ARG;
+  DeviceGuard dg(ctx);
+  if (num_layers <= 0) return fail(ctx, NVA_E_ARG, "numLayers must be > 0");
+  if (block_size <= 0 || num_kv_heads <= 0 || !head_dims)
+    return fail(ctx, NVA_E_ARG, "blockSize, numKvHeads must be > 0 and headDims non-null");
+  if (!(fraction > 0.0f && fraction <= 1.0f))
+    return fail(ctx, NVA_E_ARG, "kvHeapFraction must be in (0, 1], got %g", (double)fraction);
+  // Bytes of one page across the layers that get pages: K and V, Config.java:105-114.
+  int64_t per_block = 0;
+  for (int i = 0; i < num_layers; i++) {
+    if (allocate && !allocate[i]) continue;
+    if (head_dims[i] <= 0) return fail(ctx, NVA_E_ARG, "headDims[%d] must be > 0", i);
+    per_block += 2 * (int64_t)block_size * num_kv_heads * head_dims[i] * 4;
+  }
+  if (per_block <= 0) return fail(ctx, NVA_E_ARG, "no layer gets pages");
+  size_t free_b = 0, total_b = 0;
+  HIP_TRY(ctx, hipMemGetInfo(&free_b, &total_b), "device memory query");
+  // (long) (free * kvHeapFraction) / bytesPerBlock, at least 32 (Config.java:115-116).
+  const int64_t budget = (int64_t)((double)free_b * (double)fraction);
+  const int64_t cap = std::max<int64_t>(32, budget / per_block);
+  *blocks = (int)std::min<int64_t>(cap, INT32_MAX);
+  if (free_bytes) *free_bytes = (int64_t)free_b;
   return NVA_OK;
 }
 

@@ -111,6 +111,8 @@ SIGNATURES = {
     "nva_ctx_reset_stats": ([_vp], _st),
     "nva_kv_create": ([_vp, _ci, _ci, _ci, _ci, _vp, _vp, _pvp], _st),
     "nva_kv_destroy": ([_vp], _st),
+    "nva_kv_blocks_that_fit": ([_vp, _ci, _ci, _ci, _vp, _vp, _cf, ctypes.POINTER(_ci),
+                                ctypes.POINTER(_i64)], _st),
     "nva_kv_layer": ([_vp, _ci, _pvp, _pvp, ctypes.POINTER(_i64)], _st),
     "nva_kv_write": ([_vp, _ci, _ci, _i64, _vp, _i64], _st),
     "nva_kv_read": ([_vp, _ci, _ci, _i64, _vp, _i64], _st),

@@ -266,6 +266,43 @@ class KvCacheArena:
     def handle(self):
         return self._h
 
+    @staticmethod
+    def blocks_that_fit(ctx: Context, num_layers: int, block_size: int, num_kv_heads: int,
+                        head_dim: int = 0, head_dims: Sequence[int] = None,
+                        allocate: Sequence[bool] = None, fraction: float = 0.9):
+        """(pages that fit in ``fraction`` of the device's free HBM, the free bytes it used):
+        the heap cap of Config.resolveNumKvcacheBlocks (Config.java:93-125) with HBM in place of
+        the Java heap."""
+        if head_dims is None:
+            head_dims = [head_dim] * num_layers
+        if allocate is None:
+            allocate = [True] * len(head_dims)
+        hd = np.asarray(head_dims, np.int32)
+        al = np.asarray([1 if a else 0 for a in allocate], np.uint8)
+        blocks = ctypes.c_int()
+        free = ctypes.c_int64()
+        _check(ctx.handle, N.load().nva_kv_blocks_that_fit(
+            ctx.handle, len(hd), block_size, num_kv_heads, _ptr(hd), _ptr(al),
+            ctypes.c_float(fraction), ctypes.byref(blocks), ctypes.byref(free)),
+            "KvCacheArena.blocks_that_fit")
+        return blocks.value, free.value
+
+    @staticmethod
+    def resolve_num_blocks(ctx: Context, configured: int, max_num_seqs: int, max_model_len: int,
+                           block_size: int, num_kv_heads: int, head_dims: Sequence[int],
+                           allocate: Sequence[bool] = None, fraction: float = 0.9) -> int:
+        """Config.resolveNumKvcacheBlocks (Config.java:93-125) for a device arena: the configured
+        count if positive, else min(max(maxNumSeqs * ceil(maxModelLen / blockSize), 128), the
+        pages that fit in ``fraction`` of the free HBM)."""
+        if configured > 0:
+            return configured
+        per_seq = (max_model_len + block_size - 1) // block_size
+        estimated = max(max_num_seqs * per_seq, 128)
+        cap, _ = KvCacheArena.blocks_that_fit(ctx, len(head_dims), block_size, num_kv_heads,
+                                              head_dims=head_dims, allocate=allocate,
+                                              fraction=fraction)
+        return min(estimated, cap)
+
     def _layer(self, layer: int):
         k = ctypes.c_void_p()
         v = ctypes.c_void_p()
