@@ -34,6 +34,8 @@
 //     MFMAs run.
 //   * Output block layout (32 x 32, 16 values per lane): value r of lane (i, h) is row
 //     8 * (r / 4) + 4 * h + r % 4, column i -- lanes 0..31 write 128 contiguous bytes.
+//   * Tiles are assigned so that each XCD's workgroups cover one rectangle of the tile grid
+//     (xcd_tile below): each XCD's L2 then fetches only its share of x and of W.
 //   * When the grid alone cannot fill the chip, K is split over blockIdx.z (both MFMA
 //     kernels); slices write partial sums and linear_reduce_kernel adds them in slice order,
 //     plus the bias.  (Letting the last slice of a tile reduce in place needs a device-scope
@@ -54,6 +56,39 @@ constexpr int kSkinnyWaves = 8;  // waves of a skinny_kernel workgroup (two per 
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
+// Tile (column tile tn, row band tm) of this workgroup within its K slice.  Workgroups are
+// handed to the 8 XCDs round-robin by linear block id, so consecutive ids would spread every
+// 128-row band of x over all eight L2s, each fetching it again.  When the tile grid divides
+// into 8 equal rectangles of gm row bands x gn column tiles (gm * gn = 8), XCD slot t % 8 runs
+// rectangle t % 8 and t / 8 walks it row-major: each L2 then fetches 1/gm of x and 1/gn of W.
+// gm minimises that sum (x bands are BM rows, W tiles BN rows; ties go to the smaller gm: at
+// 4096 x 2048 -> 1024, 4 x 2 rectangles fetched 65 MB against 81 MB as 8 x 1 bands and 142 MB
+// in launch order, in the same time).  Any other grid keeps the launch order.  A bijection
+// either way, so the result does not depend on where a workgroup actually runs.
+__device__ __forceinline__ void xcd_tile(int &tn, int &tm) {
+  const int nt = gridDim.x, mt = gridDim.y;
+  int gm = 0, best = 0x7fffffff;
+  for (int c = 1; c <= 8; c <<= 1) {
+    if (mt % c != 0 || nt % (8 / c) != 0) continue;
+    const int cost = mt / c * BM + nt / (8 / c) * BN;
+    if (cost < best) {
+      best = cost;
+      gm = c;
+    }
+  }
+  const int t = blockIdx.y * nt + blockIdx.x;
+  if (gm == 0) {
+    tm = blockIdx.y;
+    tn = blockIdx.x;
+    return;
+  }
+  const int gn = 8 / gm, rh = mt / gm, cw = nt / gn;
+  const int x = t & 7, r = t >> 3;
+  const int lr = r / cw;
+  tm = (x / gn) * rh + lr;
+  tn = (x % gn) * cw + (r - lr * cw);
+}
+
 template <int N> struct IntC { static constexpr int value = N; };
 template <bool B> struct BoolC { static constexpr bool value = B; };
 
@@ -67,8 +102,10 @@ __global__ void __launch_bounds__(256) linear_kernel(LinearLaunch a) {
   constexpr int STAGE = (BM + BN) * BK;      // floats: A rows, then B rows
   __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
 
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
+  int tn, tm;
+  xcd_tile(tn, tm);
+  const int n0 = tn * BN;
+  const int m0 = tm * BM;
   const int kb = blockIdx.z * a.k_per_split;
   const int ke = min(a.k, kb + a.k_per_split);
   const int ntiles = (ke - kb + BK - 1) / BK;
