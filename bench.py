@@ -54,6 +54,11 @@ def parse():
                     help="time o_proj (nva_linear_forward, the library's own kernels) and "
                          "torch.addmm (hipBLASLt) on the decode and prefill o_proj shapes, one "
                          "JSON line per shape")
+    ap.add_argument("--cu-share", type=int, default=0, metavar="K",
+                    help="with --workload: run it on a stream limited to K/16 of the CUs "
+                         "(hipExtStreamCreateWithCUMask, 2K of the mask's 32 groups of 8 bits), "
+                         "for the per-CU bandwidth of a kernel (a mixed step's second stream "
+                         "and the graph replays are not limited); the line gains the CU count")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device-to-device copy three times (the "
                          "known-size reference for the FETCH_SIZE/WRITE_SIZE counters)")
@@ -153,6 +158,56 @@ def kernel_a_bytes(wl, k_out):
     T, hq, hkv, d = wl.tokens, wl.hq, wl.hkv, wl.d
     return T * (4 * d * (hq + 2 * hkv) + 4 * d * (hq + (hkv if k_out else 0)) +
                 4 * d * 2 * hkv + 4 * d + 8)
+
+
+class cu_masked_stream:
+    """A HIP stream restricted to `share`/16 of the device's CUs.  The mask's bits are taken in
+    groups of 8 consecutive bits, 2 * share of every 32 groups, spread evenly: each XCD keeps the
+    same share of its CUs whether the runtime numbers the bits XCD by XCD or hands consecutive
+    bits to the 8 XCDs in turn (with bits i % 16 < share, share 12 ran slower than 8 and share 6
+    could not create the stream).  Yields the stream (as a torch ExternalStream) and the number
+    of CUs it may use.  The HIP runtime is the one this process already loaded (found in
+    /proc/self/maps), so the stream belongs to it."""
+
+    def __init__(self, share):
+        if not 1 <= share <= 16:
+            raise SystemExit("--cu-share takes 1..16")
+        self.share = share
+
+    def __enter__(self):
+        import ctypes
+        import torch
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        if path is None:
+            raise SystemExit("libamdhip64.so is not loaded")
+        self.hip = ctypes.CDLL(path)
+        n = torch.cuda.get_device_properties(0).multi_processor_count
+        words = (n + 31) // 32
+        mask = (ctypes.c_uint32 * words)()
+        cus = 0
+        groups = (n + 7) // 8
+        sel = groups * self.share // 16  # groups selected, spread evenly over the mask
+        for i in range(n):
+            gi = i // 8
+            if ((gi + 1) * sel) // groups > (gi * sel) // groups:
+                mask[i // 32] |= 1 << (i % 32)
+                cus += 1
+        self.s = ctypes.c_void_p()
+        rc = self.hip.hipExtStreamCreateWithCUMask(ctypes.byref(self.s), ctypes.c_uint32(n), mask)
+        if rc != 0:
+            raise SystemExit(f"hipExtStreamCreateWithCUMask failed: {rc}")
+        return torch.cuda.ExternalStream(self.s.value), cus
+
+    def __exit__(self, *exc):
+        import torch
+        torch.cuda.synchronize()
+        self.hip.hipStreamDestroy(self.s)
+        return False
 
 
 def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, label,
@@ -682,7 +737,18 @@ def main():
         ctx.close()
         return
     if args.workload:
-        line = bench_extra(args, ctx)
+        if args.cu_share:
+            with cu_masked_stream(args.cu_share) as (ext, cus):
+                with torch.cuda.stream(ext):
+                    ctx.set_stream(ext)
+                    line = bench_extra(args, ctx)
+                    torch.cuda.synchronize()
+                    ctx.set_stream()
+            line["cu_share"] = {"sixteenths": args.cu_share, "cus": cus}
+            if "decode_rows" in line:
+                line["cu_share"]["decode_gbs_per_cu"] = round(line["decode_rows"]["gbs"] / cus, 2)
+        else:
+            line = bench_extra(args, ctx)
         ctx.close()
         print(json.dumps(line), flush=True)
         return

@@ -412,9 +412,11 @@ int largest_pow2_divisor_upto(int rep, int cap) {
 // CUs for the tile grid of a mixed plan, one tile workgroup on each; the rows run on the other
 // CUs and in the room left on the tile CUs.  The tile share f of the CUs minimises the longer of
 // the two kernels: the tiles' time scales as 1/f, while the rows, being HBM-bound, keep
-// 1 - f^1.8 of the whole chip's bandwidth on the remaining CUs (the split-KV decode on
-// CU-masked streams holds 72% of it on half of the CUs, 60% on 3/8, 42% on 1/4).  Solo rates:
-// rows 6.5 TB/s, tiles 100 / 80 / 70 TFLOP/s at head dim <= 128 / 256 / 512.
+// 1 - f^1.8 of the whole chip's bandwidth.  That is below what the rows keep alone on the
+// remaining CUs of a CU-masked stream (85% on half of the CUs, 68% on 3/8, 49% on 1/4), since
+// beside tile workgroups they lose bandwidth too; for the Qwen3-4B-like mixed step it picks 160
+// CUs, the best of a sweep over 128..208.  Solo rates: rows 6.5 TB/s, tiles 100 / 80 / 70
+// TFLOP/s at head dim <= 128 / 256 / 512.
 int64_t mixed_tile_cus(int num_cus, double row_bytes, double tile_flops, int head_dim) {
   const double tr = row_bytes / 6.5e12;
   const double tt =
