@@ -543,11 +543,11 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
   plan->covers_all = covered == key.tokens;
 
   // Stream-K schedule of the MFMA tiles.  The grid has exactly as many workgroups per head
-  // group ("slots") as can be resident at once; the 32-key tiles of all query tiles, laid end
-  // to end, are cut into equal runs, one per slot, so every slot finishes at the same time.  A
-  // query tile whose keys fall into several runs becomes several segments; they write partials
-  // (query-major, segment-minor) that the merge kernel combines.  A segment also never spans
-  // more pages than the kernel's LDS copy of the block table holds.
+  // group ("slots") as can be resident at once; the 32-key tiles of all query tiles are cut
+  // into equal runs, one per slot, so every slot finishes at the same time.  A query tile whose
+  // keys fall into several runs becomes several segments; they write partials (query-major,
+  // segment-minor) that the merge kernel combines.  A segment also never spans more pages than
+  // the kernel's LDS copy of the block table holds.
   std::vector<MergeItem> merges;
   std::vector<int32_t> seg_off;
   int parts = 0;
@@ -577,36 +577,143 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     slots = (int)std::max<int64_t>(1, std::min<int64_t>(total, resident / key.tile_groups));
     const int64_t page_cap =
         paged ? (int64_t)(kPrefillTablePages - 2) * key.block_size / KT * KT : INT32_MAX;
-    std::vector<std::vector<TileItem>> per_slot(slots);
-    int64_t pos = 0;  // first key tile of the current query tile in the flattened order
-    for (const TileItem &t : tiles) {
-      const int64_t n = (t.ke - t.ks + KT - 1) / KT;
-      // Pieces: cut at slot boundaries (slot s owns [s*total/slots, (s+1)*total/slots)) and at
-      // the page cap.
-      std::vector<std::pair<int, std::pair<int, int>>> pieces;  // slot, [ks, ke)
-      int64_t j = 0;
-      while (j < n) {
-        const int64_t g = pos + j;
-        const int s_of = (int)std::min<int64_t>(slots - 1, g * slots / total);
-        const int64_t s_end = ((int64_t)(s_of + 1) * total + slots - 1) / slots;  // exclusive
-        int64_t take = std::min<int64_t>(n - j, s_end - g);
-        take = std::max<int64_t>(1, std::min<int64_t>(take, page_cap / KT));
-        const int k0 = t.ks + (int)(j * KT);
-        const int k1 = std::min<int>(t.ke, t.ks + (int)((j + take) * KT));
-        pieces.push_back({s_of, {k0, k1}});
-        j += take;
+    // Two ways to cut the tiles into equal runs; the plan keeps the one that splits fewer
+    // query rows (each split row writes and re-reads one partial per segment), unless that one
+    // cuts a tile into more segments than the row-wide merge folds:
+    //  (a) the query tiles in sequence order, laid end to end, cut at every slot boundary;
+    //  (b) tiles longer than a run (cap = ceil(total / slots) key tiles) first, largest first,
+    //      each filling whole empty slots and its remainder going to the fullest slot it fits;
+    //      then the other tiles whole, largest first, each into the fullest slot it fits; what
+    //      is left goes, piece by piece, to the emptiest slot.
+    // Both give every slot the same number of key tiles (to one).  Measured splits (rows):
+    // C2's shape 6784 (a) / 5696 (b), Gemma3 d = 256 global 11648 / 8192, with a 512-key
+    // window 9472 / 8832.
+    struct Piece {
+      int slot, k0, k1;
+    };
+    const int64_t cap_tiles = std::max<int64_t>(1, page_cap / KT);
+    const int nt = (int)tiles.size();
+    std::vector<int64_t> ntile(nt);
+    for (int i = 0; i < nt; i++) ntile[i] = (tiles[i].ke - tiles[i].ks + KT - 1) / KT;
+    auto split_rows = [&](const std::vector<std::vector<Piece>> &pc) {
+      int64_t r = 0;
+      for (int i = 0; i < nt; i++)
+        if (pc[i].size() > 1)
+          r += (int64_t)pc[i].size() * std::min(key.tile_q, tiles[i].qlen - tiles[i].q0);
+      return r;
+    };
+    auto max_pieces = [&](const std::vector<std::vector<Piece>> &pc) {
+      size_t m = 1;
+      for (const auto &v : pc) m = std::max(m, v.size());
+      return (int)m;
+    };
+    std::vector<std::vector<Piece>> cut_a(nt), cut_b(nt);
+    {
+      int64_t pos = 0;  // first key tile of the current query tile in the flattened order
+      for (int i = 0; i < nt; i++) {
+        const TileItem &t = tiles[i];
+        const int64_t n = ntile[i];
+        int64_t j = 0;
+        while (j < n) {
+          const int64_t g = pos + j;
+          const int s_of = (int)std::min<int64_t>(slots - 1, g * slots / total);
+          const int64_t s_end = ((int64_t)(s_of + 1) * total + slots - 1) / slots;  // exclusive
+          int64_t take = std::min<int64_t>(n - j, s_end - g);
+          take = std::max<int64_t>(1, std::min<int64_t>(take, cap_tiles));
+          cut_a[i].push_back({s_of, t.ks + (int)(j * KT),
+                              std::min<int>(t.ke, t.ks + (int)((j + take) * KT))});
+          j += take;
+        }
+        pos += n;
       }
-      pos += n;
-      const int np = (int)pieces.size();
+    }
+    {
+      const int64_t cap = (total + slots - 1) / slots;
+      std::vector<int64_t> load(slots, 0);
+      std::vector<std::vector<std::pair<int, int64_t>>> runs(nt);  // (slot, key tiles)
+      std::vector<int64_t> rem(nt, 0);
+      std::vector<int> order(nt);
+      for (int i = 0; i < nt; i++) order[i] = i;
+      std::stable_sort(order.begin(), order.end(),
+                       [&](int x, int y) { return ntile[x] > ntile[y]; });
+      auto fullest_fit = [&](int64_t n) {
+        int best = -1;
+        for (int b = 0; b < slots; b++)
+          if (load[b] + n <= cap && (best < 0 || load[b] > load[best])) best = b;
+        return best;
+      };
+      int empty = 0;  // slots below this index are not empty
+      for (int i : order) {
+        if (ntile[i] <= cap) continue;
+        rem[i] = ntile[i];
+        while (rem[i] >= cap) {
+          while (empty < slots && load[empty] != 0) empty++;
+          if (empty == slots) break;
+          load[empty] = cap;
+          runs[i].push_back({empty, cap});
+          rem[i] -= cap;
+        }
+        if (rem[i] > 0) {
+          const int b = fullest_fit(rem[i]);
+          if (b >= 0) {
+            load[b] += rem[i];
+            runs[i].push_back({b, rem[i]});
+            rem[i] = 0;
+          }
+        }
+      }
+      for (int i : order) {
+        if (ntile[i] > cap) continue;
+        const int b = fullest_fit(ntile[i]);
+        if (b >= 0) {
+          load[b] += ntile[i];
+          runs[i].push_back({b, ntile[i]});
+        } else {
+          rem[i] = ntile[i];
+        }
+      }
+      for (int i : order)
+        while (rem[i] > 0) {
+          int b = 0;
+          for (int x = 1; x < slots; x++)
+            if (load[x] < load[b]) b = x;
+          const int64_t take = load[b] < cap ? std::min<int64_t>(rem[i], cap - load[b]) : rem[i];
+          load[b] += take;
+          runs[i].push_back({b, take});
+          rem[i] -= take;
+        }
+      // Runs to key ranges, in key order; runs longer than the page cap split in their slot.
+      for (int i = 0; i < nt; i++) {
+        const TileItem &t = tiles[i];
+        int64_t off = 0;
+        for (const auto &r : runs[i]) {
+          int64_t c = r.second;
+          while (c > 0) {
+            const int64_t take = std::min<int64_t>(c, cap_tiles);
+            cut_b[i].push_back({r.first, t.ks + (int)(off * KT),
+                                std::min<int>(t.ke, t.ks + (int)((off + take) * KT))});
+            off += take;
+            c -= take;
+          }
+        }
+      }
+    }
+    const bool use_b = split_rows(cut_b) < split_rows(cut_a) &&
+                       max_pieces(cut_b) <= std::max(kMergeRowsMaxParts, max_pieces(cut_a));
+    const std::vector<std::vector<Piece>> &cut = use_b ? cut_b : cut_a;
+    std::vector<std::vector<TileItem>> per_slot(slots);
+    for (int i = 0; i < nt; i++) {
+      const TileItem &t = tiles[i];
+      const int np = (int)cut[i].size();
       const int rows = std::min(key.tile_q, t.qlen - t.q0);
       for (int pi = 0; pi < np; pi++) {
         TileItem c = t;
-        c.ks = pieces[pi].second.first;
-        c.ke = pieces[pi].second.second;
+        c.ks = cut[i][pi].k0;
+        c.ke = cut[i][pi].k1;
         c.part = np > 1 ? parts : -1;
         c.nsplit = np;
         c.split = pi;
-        per_slot[pieces[pi].first].push_back(c);
+        per_slot[cut[i][pi].slot].push_back(c);
       }
       if (np > 1) {
         for (int r = 0; r < rows; r++) merges.push_back({t.qstart + t.q0 + r, parts + r * np, np, 0});

@@ -395,38 +395,41 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   }
 }
 
-// Row-wide merge for plans whose split rows have at most kMergeRowsMaxParts partials (prefill
-// segments): one workgroup per row covers all heads, each thread folding the partials of one
-// float4 of one head in order.  All of a thread's partial loads are issued before the first is
-// used, so the merge costs one memory round trip instead of two per partial.
-constexpr int kMergeRowsMaxParts = 4;
+// Row-wide merge for plans whose split rows have at most MP (4 or 8, kMergeRowsMaxParts)
+// partials (prefill segments): one workgroup per row covers all heads, each thread folding the
+// partials of one float4 of one head in order.  All of a thread's partial loads are issued
+// before the first is used, so the merge costs one memory round trip instead of two per
+// partial.
+template <int MP>
 __global__ void __launch_bounds__(256) merge_rows_kernel(MergeLaunch a) {
   const MergeItem it = a.items[blockIdx.x];
   const int d4 = a.head_dim >> 2;
-  const int n = it.nparts;  // 0 .. kMergeRowsMaxParts
+  const int n = it.nparts;  // 0 .. MP
   for (int idx = threadIdx.x; idx < a.hq * d4; idx += blockDim.x) {
     const int h = idx / d4;
     const int cc = idx - h * d4;
     float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
     if (n > 0) {
-      float pm[kMergeRowsMaxParts], pl[kMergeRowsMaxParts];
-      float4 px[kMergeRowsMaxParts];
+      float pm[MP], pl[MP];
+      float4 px[MP];
 #pragma unroll
-      for (int p = 0; p < kMergeRowsMaxParts; p++) {
-        const size_t pi = (size_t)(it.first + (p < n ? p : 0)) * a.hq + h;  // p < n: in range
-        pm[p] = a.part_m[pi];
-        pl[p] = a.part_l[pi];
-        px[p] = ld4(a.part_acc + pi * a.head_dim + cc * 4);
+      for (int p = 0; p < MP; p++) {
+        if (p < n) {
+          const size_t pi = (size_t)(it.first + p) * a.hq + h;
+          pm[p] = a.part_m[pi];
+          pl[p] = a.part_l[pi];
+          px[p] = ld4(a.part_acc + pi * a.head_dim + cc * 4);
+        }
       }
       float M = -INFINITY;
 #pragma unroll
-      for (int p = 0; p < kMergeRowsMaxParts; p++)
+      for (int p = 0; p < MP; p++)
         if (p < n) M = fmaxf(M, pm[p]);
       const float Ms = M == -INFINITY ? 0.0f : M;
       float L = 0.0f;
       float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int p = 0; p < kMergeRowsMaxParts; p++) {
+      for (int p = 0; p < MP; p++) {
         if (p < n) {
           const float e = __builtin_amdgcn_exp2f(pm[p] - Ms);
           L = fmaf(pl[p], e, L);
@@ -588,8 +591,11 @@ hipError_t launch_merge(const MergeLaunch &a, int max_parts, hipStream_t s) {
   if (a.num_items <= 0) return hipSuccess;
   if (a.head_dim > 512 || (a.head_dim & 3)) return hipErrorInvalidValue;
   // Few partials per row: one row-wide workgroup per row; many: spread them over 4 or 16 waves.
-  if (max_parts <= kMergeRowsMaxParts)
-    hipLaunchKernelGGL(merge_rows_kernel, dim3(a.num_items), dim3(256), 0, s, a);
+  if (max_parts <= 4)
+    hipLaunchKernelGGL(merge_rows_kernel<4>, dim3(a.num_items), dim3(256), 0, s, a);
+  else if (max_parts <= kMergeRowsMaxParts)
+    hipLaunchKernelGGL(merge_rows_kernel<kMergeRowsMaxParts>, dim3(a.num_items), dim3(256), 0,
+                       s, a);
   else if (max_parts <= 32)
     hipLaunchKernelGGL((merge_kernel<4>), dim3(a.num_items, a.hq), dim3(256), 0, s, a);
   else

@@ -183,6 +183,9 @@ int prefill_blocks_per_cu(int head_dim, int heads_per_wg);
 constexpr int kPrefillTablePages = 128;
 // Most pages one row-kernel work item may span (its block ids are staged in LDS).
 constexpr int kRowTablePages = 64;
+// Most partials per row that launch_merge folds with its row-wide kernel (one workgroup per
+// query row, all heads); rows with more take the per-(row, head) merge.
+constexpr int kMergeRowsMaxParts = 8;
 
 // Waves per prefill workgroup at this head dim (each wave owns 16 queries of one head; at
 // d = 512 a pair of waves shares them, one half of the head dims each).
