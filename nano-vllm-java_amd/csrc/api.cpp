@@ -588,26 +588,31 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     // Both give every slot the same number of key tiles (to one).  Measured splits (rows):
     // C2's shape 6784 (a) / 5696 (b), Gemma3 d = 256 global 11648 / 8192, with a 512-key
     // window 9472 / 8832.
+    // Pieces of both cuts in flat arrays, grouped by tile in key order (the plan is rebuilt
+    // every step, so it avoids a small allocation per tile).
     struct Piece {
-      int slot, k0, k1;
+      int tile, slot, k0, k1;
     };
     const int64_t cap_tiles = std::max<int64_t>(1, page_cap / KT);
     const int nt = (int)tiles.size();
     std::vector<int64_t> ntile(nt);
     for (int i = 0; i < nt; i++) ntile[i] = (tiles[i].ke - tiles[i].ks + KT - 1) / KT;
-    auto split_rows = [&](const std::vector<std::vector<Piece>> &pc) {
-      int64_t r = 0;
-      for (int i = 0; i < nt; i++)
-        if (pc[i].size() > 1)
-          r += (int64_t)pc[i].size() * std::min(key.tile_q, tiles[i].qlen - tiles[i].q0);
-      return r;
+    // Rows written as partials, and the most segments of one tile.
+    auto score = [&](const std::vector<Piece> &pc, int64_t *rows, int *most) {
+      *rows = 0;
+      *most = 1;
+      for (size_t a = 0; a < pc.size();) {
+        size_t b = a;
+        while (b < pc.size() && pc[b].tile == pc[a].tile) b++;
+        const int np = (int)(b - a);
+        const TileItem &t = tiles[pc[a].tile];
+        if (np > 1) *rows += (int64_t)np * std::min(key.tile_q, t.qlen - t.q0);
+        *most = std::max(*most, np);
+        a = b;
+      }
     };
-    auto max_pieces = [&](const std::vector<std::vector<Piece>> &pc) {
-      size_t m = 1;
-      for (const auto &v : pc) m = std::max(m, v.size());
-      return (int)m;
-    };
-    std::vector<std::vector<Piece>> cut_a(nt), cut_b(nt);
+    std::vector<Piece> cut_a, cut_b;
+    cut_a.reserve(nt + slots);
     {
       int64_t pos = 0;  // first key tile of the current query tile in the flattened order
       for (int i = 0; i < nt; i++) {
@@ -620,8 +625,8 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
           const int64_t s_end = ((int64_t)(s_of + 1) * total + slots - 1) / slots;  // exclusive
           int64_t take = std::min<int64_t>(n - j, s_end - g);
           take = std::max<int64_t>(1, std::min<int64_t>(take, cap_tiles));
-          cut_a[i].push_back({s_of, t.ks + (int)(j * KT),
-                              std::min<int>(t.ke, t.ks + (int)((j + take) * KT))});
+          cut_a.push_back({i, s_of, t.ks + (int)(j * KT),
+                           std::min<int>(t.ke, t.ks + (int)((j + take) * KT))});
           j += take;
         }
         pos += n;
@@ -629,9 +634,13 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     }
     {
       const int64_t cap = (total + slots - 1) / slots;
-      std::vector<int64_t> load(slots, 0);
-      std::vector<std::vector<std::pair<int, int64_t>>> runs(nt);  // (slot, key tiles)
-      std::vector<int64_t> rem(nt, 0);
+      std::vector<int64_t> load(slots, 0), rem(nt, 0);
+      struct Run {
+        int tile, slot;
+        int64_t n;
+      };
+      std::vector<Run> runs;
+      runs.reserve(nt + 2 * slots);
       std::vector<int> order(nt);
       for (int i = 0; i < nt; i++) order[i] = i;
       std::stable_sort(order.begin(), order.end(),
@@ -650,14 +659,14 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
           while (empty < slots && load[empty] != 0) empty++;
           if (empty == slots) break;
           load[empty] = cap;
-          runs[i].push_back({empty, cap});
+          runs.push_back({i, empty, cap});
           rem[i] -= cap;
         }
         if (rem[i] > 0) {
           const int b = fullest_fit(rem[i]);
           if (b >= 0) {
             load[b] += rem[i];
-            runs[i].push_back({b, rem[i]});
+            runs.push_back({i, b, rem[i]});
             rem[i] = 0;
           }
         }
@@ -667,7 +676,7 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
         const int b = fullest_fit(ntile[i]);
         if (b >= 0) {
           load[b] += ntile[i];
-          runs[i].push_back({b, ntile[i]});
+          runs.push_back({i, b, ntile[i]});
         } else {
           rem[i] = ntile[i];
         }
@@ -679,54 +688,61 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
             if (load[x] < load[b]) b = x;
           const int64_t take = load[b] < cap ? std::min<int64_t>(rem[i], cap - load[b]) : rem[i];
           load[b] += take;
-          runs[i].push_back({b, take});
+          runs.push_back({i, b, take});
           rem[i] -= take;
         }
       // Runs to key ranges, in key order; runs longer than the page cap split in their slot.
-      for (int i = 0; i < nt; i++) {
-        const TileItem &t = tiles[i];
-        int64_t off = 0;
-        for (const auto &r : runs[i]) {
-          int64_t c = r.second;
-          while (c > 0) {
-            const int64_t take = std::min<int64_t>(c, cap_tiles);
-            cut_b[i].push_back({r.first, t.ks + (int)(off * KT),
-                                std::min<int>(t.ke, t.ks + (int)((off + take) * KT))});
-            off += take;
-            c -= take;
-          }
+      std::stable_sort(runs.begin(), runs.end(),
+                       [](const Run &x, const Run &y) { return x.tile < y.tile; });
+      cut_b.reserve(runs.size());
+      int64_t off = 0;
+      for (size_t r = 0; r < runs.size(); r++) {
+        if (r == 0 || runs[r].tile != runs[r - 1].tile) off = 0;
+        const TileItem &t = tiles[runs[r].tile];
+        int64_t c = runs[r].n;
+        while (c > 0) {
+          const int64_t take = std::min<int64_t>(c, cap_tiles);
+          cut_b.push_back({runs[r].tile, runs[r].slot, t.ks + (int)(off * KT),
+                           std::min<int>(t.ke, t.ks + (int)((off + take) * KT))});
+          off += take;
+          c -= take;
         }
       }
     }
-    const bool use_b = split_rows(cut_b) < split_rows(cut_a) &&
-                       max_pieces(cut_b) <= std::max(kMergeRowsMaxParts, max_pieces(cut_a));
-    const std::vector<std::vector<Piece>> &cut = use_b ? cut_b : cut_a;
-    std::vector<std::vector<TileItem>> per_slot(slots);
-    for (int i = 0; i < nt; i++) {
-      const TileItem &t = tiles[i];
-      const int np = (int)cut[i].size();
+    int64_t rows_a = 0, rows_b = 0;
+    int most_a = 1, most_b = 1;
+    score(cut_a, &rows_a, &most_a);
+    score(cut_b, &rows_b, &most_b);
+    const std::vector<Piece> &cut =
+        rows_b < rows_a && most_b <= std::max(kMergeRowsMaxParts, most_a) ? cut_b : cut_a;
+    // Segments grouped by slot (counting sort), each slot's in tile order.
+    std::vector<int32_t> fill(slots + 1, 0);
+    for (const Piece &pc : cut) fill[pc.slot + 1]++;
+    for (int sl = 0; sl < slots; sl++) fill[sl + 1] += fill[sl];
+    seg_off.assign(fill.begin(), fill.end());
+    std::vector<TileItem> segs(cut.size());
+    for (size_t a = 0; a < cut.size();) {
+      size_t b = a;
+      while (b < cut.size() && cut[b].tile == cut[a].tile) b++;
+      const TileItem &t = tiles[cut[a].tile];
+      const int np = (int)(b - a);
       const int rows = std::min(key.tile_q, t.qlen - t.q0);
       for (int pi = 0; pi < np; pi++) {
         TileItem c = t;
-        c.ks = cut[i][pi].k0;
-        c.ke = cut[i][pi].k1;
+        c.ks = cut[a + pi].k0;
+        c.ke = cut[a + pi].k1;
         c.part = np > 1 ? parts : -1;
         c.nsplit = np;
         c.split = pi;
-        per_slot[cut[i][pi].slot].push_back(c);
+        segs[fill[cut[a + pi].slot]++] = c;
       }
       if (np > 1) {
         for (int r = 0; r < rows; r++) merges.push_back({t.qstart + t.q0 + r, parts + r * np, np, 0});
         parts += rows * np;
       }
+      a = b;
     }
-    tiles.clear();
-    seg_off.reserve(slots + 1);
-    for (int sl = 0; sl < slots; sl++) {
-      seg_off.push_back((int32_t)tiles.size());
-      tiles.insert(tiles.end(), per_slot[sl].begin(), per_slot[sl].end());
-    }
-    seg_off.push_back((int32_t)tiles.size());
+    tiles.swap(segs);
   }
 
   // Chunk: the largest of 4096..64 keys that still gives the grid >= 8 workgroups per CU.  On
