@@ -184,7 +184,8 @@ constexpr int kPrefillTablePages = 128;
 // Most pages one row-kernel work item may span (its block ids are staged in LDS).
 constexpr int kRowTablePages = 64;
 // Most partials per row that launch_merge folds with its row-wide kernel (one workgroup per
-// query row, all heads); rows with more take the per-(row, head) merge.
+// query row, all heads) when a plan has many merge rows; rows with more take the per-(row,
+// head) merge.
 constexpr int kMergeRowsMaxParts = 8;
 
 // Waves per prefill workgroup at this head dim (each wave owns 16 queries of one head; at
