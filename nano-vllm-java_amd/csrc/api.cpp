@@ -586,8 +586,8 @@ nva_status get_plan(nva_ctx *ctx, const PlanKey &key, Plan **out) {
     //      then the other tiles whole, largest first, each into the fullest slot it fits; what
     //      is left goes, piece by piece, to the emptiest slot.
     // Both give every slot the same number of key tiles (to one).  Measured splits (rows):
-    // C2's shape 6784 (a) / 5696 (b), Gemma3 d = 256 global 11648 / 8192, with a 512-key
-    // window 9472 / 8832.
+    // Qwen3-0.6B varlen prefill 512/1024/1536/2048 6784 (a) / 5696 (b), Gemma3 d = 256 global
+    // 11648 / 8192, with a 512-key window 9472 / 8832.
     // Pieces of both cuts in flat arrays, grouped by tile in key order (the plan is rebuilt
     // every step, so it avoids a small allocation per tile).
     struct Piece {

@@ -593,7 +593,7 @@ hipError_t launch_merge(const MergeLaunch &a, int max_parts, hipStream_t s) {
   // Few partials per row: one row-wide workgroup per row; many: spread them over 4 or 16 waves.
   // Rows with 5..8 partials take the row-wide form only when there are enough rows to fill the
   // chip (prefill segments); a decode step's few rows merge faster with a workgroup per (row,
-  // head) (C1: 6.3-6.7 against 6.2-6.3 us after a flush).
+  // head) (Qwen3 decode of 8 rows: 6.3-6.7 against 6.2-6.3 us after a flush).
   if (max_parts <= 4)
     hipLaunchKernelGGL(merge_rows_kernel<4>, dim3(a.num_items), dim3(256), 0, s, a);
   else if (max_parts <= kMergeRowsMaxParts && a.num_items >= 512)
