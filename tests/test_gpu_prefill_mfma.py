@@ -93,3 +93,24 @@ def test_tile_copies_across_pages(ctx, d, block_size, window):
     finally:
         ctx.set_timing(False)
     assert launches >= 1, "the MFMA prefill kernel did not run"
+
+
+@pytest.mark.parametrize("block_size,new", [(1, 2048), (4, 4096)])
+def test_runs_longer_than_page_cap(ctx, block_size, new):
+    """Equal runs of key tiles per slot longer than one segment may span over pages of 1 or 4
+    tokens (126 pages: 3 or 15 tiles of 32 keys): the planner cuts such a run into several
+    segments of the same query tile in the same slot, whichever of its two cuts it keeps (at
+    2048 / 4096 new tokens over 256 slots a run is 5 / 17 tiles)."""
+    rng = np.random.default_rng(block_size * 11 + new)
+    seqs = [(0, new), (700, 64)]
+    wl = W.build(f"page-capped runs bs{block_size}", seqs, is_prefill=True, hq=4, hkv=2, d=128,
+                 scale=float(np.float32(128 ** -0.5)), rng=rng, block_size=block_size,
+                 pool_cap=20000)
+    ctx.reset_stats()
+    ctx.set_timing(True)
+    try:
+        check_attention(ctx, Case(wl, seed=block_size + new), wl.name)
+        launches, _ = ctx.kernel_stats("prefill")
+    finally:
+        ctx.set_timing(False)
+    assert launches >= 1, "the MFMA prefill kernel did not run"
