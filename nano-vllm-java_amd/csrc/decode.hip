@@ -28,6 +28,7 @@
 //     chunk is written.
 // HBM bytes per work item: chunk * 2 * D * 4 per KV head (+ q, + the partial or output row).
 #include "nva_internal.h"
+#include "nva_device.h"
 
 namespace nva {
 
@@ -41,6 +42,21 @@ __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<floa
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld4_stream(const float *p) {
   const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+  return make_float4(t.x, t.y, t.z, t.w);
+}
+// The same non-temporal load from a wave-uniform base plus a 32-bit lane offset (floats), as a
+// buffer load: the base stays in scalar registers, so no per-lane 64-bit address is formed
+// (headline decode 2.160-2.162 against 2.166-2.171 ms with the pointer form).  The cache policy
+// matters, the form little: without the non-temporal bit the same loads take 2.40 ms, and
+// adding the L1-bypass (sc0) or device-scope (sc1) bits changes nothing.
+__device__ __forceinline__ float4 ld4_stream_at(const float *base, uint32_t off) {
+  constexpr int kNonTemporal = 2;  // the nt bit of the buffer instructions' cache policy
+  const uint64_t b = (uint64_t)(size_t)base;
+  const uint64_t u = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(size_t)u, (short)0, 0x7fffffff, kBufferWord3);
+  const f32x4 t = __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, kNonTemporal);
   return make_float4(t.x, t.y, t.z, t.w);
 }
 
@@ -227,8 +243,8 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       for (int u = 0; u < UH; u++)
 #pragma unroll
         for (int j = 0; j < VPL; j++) {
-          kr[u][j] = ld4_stream(kb + off[u] + LPT * 4 * j);
-          vr[u][j] = ld4_stream(vb + off[u] + LPT * 4 * j);
+          kr[u][j] = ld4_stream_at(kb, off[u] + LPT * 4 * j);  // kb, vb: wave-uniform
+          vr[u][j] = ld4_stream_at(vb, off[u] + LPT * 4 * j);
         }
     } else {
 #pragma unroll
