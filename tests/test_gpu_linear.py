@@ -86,10 +86,12 @@ def test_linear_matches_oracle(ctx, rows, inf, outf, bias):
 
 
 @pytest.mark.parametrize("rows,inf,outf", [(4096, 2048, 1024), (512, 4096, 2560),
-                                           (2100, 4096, 2560)])
+                                           (2100, 4096, 2560), (4000, 2048, 1000),
+                                           (8192, 2048, 1024)])
 def test_linear_full_prefill_shapes_fp64(ctx, rows, inf, outf):
     """Qwen3-0.6B o_proj over the 4096-token prefill, and Qwen3-4B-like o_projs (2100 rows: more
-    tiles than two per CU, and an M tail of 52 rows)."""
+    tiles than two per CU, and an M tail of 52 rows); M and N tails at a full grid (4000 x 1000:
+    a 32-row band and a 40-column tile) and two rounds of tiles (8192 rows)."""
     x, w, b = data(rows, inf, outf, True, 3)
     want = x.astype(np.float64) @ w.astype(np.float64).T + b
     check(run(ctx, x, w, b), want, f"linear {rows}x{inf}->{outf} vs fp64")
