@@ -121,3 +121,22 @@ def test_linear_repeatable_bit_for_bit(ctx):
         a1, a2 = run(ctx, x, w, b), run(ctx, x, w, b)
         say(f"linear {rows}x{inf}->{outf}: repeat identical={np.array_equal(a1, a2)}")
         assert np.array_equal(a1.view(np.uint32), a2.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_linear_fuzz_fp64(ctx, seed):
+    """Random shapes across the four kernels and their edges (GEMV forms, 32 x 32 blocks with K
+    slices, 128 x 64 tiles with slices, ragged M / N / K tails, grids that do and do not divide
+    into XCD rectangles), with and without bias, against a float64 product on the device."""
+    rng = np.random.default_rng(1000 + seed)
+    rows = int(rng.choice([int(rng.integers(1, 9)), int(rng.integers(9, 300)),
+                           int(rng.integers(300, 5000))]))
+    inf = 4 * int(rng.integers(1, 1100))
+    outf = int(rng.integers(1, 3000))
+    bias = bool(rng.integers(0, 2))
+    x, w, b = data(rows, inf, outf, bias, 77 + seed)
+    got = run(ctx, x, w, b)
+    want = torch.from_numpy(x).cuda().double() @ torch.from_numpy(w).cuda().double().T.contiguous()
+    if b is not None:
+        want = want + torch.from_numpy(b).cuda().double()
+    check(got, want.cpu().numpy(), f"linear fuzz {seed}: {rows}x{inf}->{outf} bias={bias}")
