@@ -20,7 +20,10 @@
  *     pointers may then be NULL (the reference returns an empty tensor).
  *   - All work is enqueued on the context's HIP stream and is asynchronous unless stated.
  *   - A context is used by one host thread at a time (the reference's single generate thread,
- *     Attention.java:41-44); there is no internal locking.
+ *     Attention.java:41-44); there is no internal locking.  Its calls share its device buffers
+ *     (plans, split partials), so their work must run in order on the device: after
+ *     nva_ctx_set_stream() to a stream not ordered with the previous one, synchronise before
+ *     the next call.
  *   - There is no CPU fallback: nva_ctx_create() fails with NVA_E_HIP when no HIP device is
  *     usable.
  */

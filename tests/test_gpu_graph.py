@@ -4,7 +4,8 @@ replayed, through the C ABI.
 The no-allocation entry point is the one meant for callers under graph capture: once a step's
 plan is in the library's scratch array, a call launches kernels only (no allocation, no plan
 copy, no memset), so its launch sequence can be captured.  Checked on a split-KV decode (store,
-row kernel, merge) and on a mixed prefill (MFMA tiles on the context's stream, qLen = 1 rows
+row kernel, merge), on one with more workgroups than the row kernel keeps resident (several
+dispatch rounds), and on a mixed prefill (MFMA tiles on the context's stream, qLen = 1 rows
 forked onto its second stream and joined with events): each replay, with eager work and
 synchronisations between the replays, gives output bit-identical to the eager call on the same
 inputs, also after the inputs the graph reads are overwritten with new values.
@@ -87,6 +88,17 @@ def test_decode_step_graph_replays():
     case = Case(W.build("decode 8 rows", [(c - 1, 1) for c in ctxs], is_prefill=False, hq=16,
                         hkv=8, d=128, scale=W.QWEN_SCALE, rng=rng), seed=41)
     run_graph(case, "decode 8 rows")
+
+
+def test_decode_many_rows_graph_replays():
+    # 1100 rows x 2 KV heads: more workgroups than the row kernel keeps resident.
+    rng = np.random.default_rng(43)
+    ctxs = [int(x) for x in rng.integers(1, 301, 1100)]
+    ctxs[:4] = [int(x) for x in rng.integers(5000, 9001, 4)]
+    case = Case(W.build("decode 1100 rows", [(c - 1, 1) for c in ctxs], is_prefill=False, hq=4,
+                        hkv=2, d=64, scale=0.125, rng=rng, block_size=16, pool_cap=1 << 20),
+                seed=43)
+    run_graph(case, "decode 1100 rows (several dispatch rounds)", replays=4)
 
 
 def test_mixed_step_graph_replays():
