@@ -558,6 +558,10 @@ void launch_row_dh(const RowLaunch &a, const dim3 &grid, hipStream_t s) {
     hipLaunchKernelGGL((row_attention_kernel<D, HPW, false>), grid, dim3(256), 0, s, a);
 }
 
+// Head counts that are not powers of two (GQA ratios 3, 5, 6, 7, e.g. 40 query heads over 8 KV
+// heads) are built for the head dims of real models only.
+constexpr bool row_odd_heads(int d) { return d >= 32 && d <= 256; }
+
 template <int D>
 hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
   const dim3 grid(a.num_items * (a.hkv * ((a.hq / a.hkv) / hpw)));
@@ -568,6 +572,18 @@ hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
     case 8:
       if constexpr (D <= 256) {
         launch_row_dh<D, 8>(a, grid, s);
+        break;
+      }
+      return hipErrorInvalidValue;
+    case 3:
+    case 5:
+    case 6:
+    case 7:
+      if constexpr (row_odd_heads(D)) {
+        if (hpw == 3) launch_row_dh<D, 3>(a, grid, s);
+        else if (hpw == 5) launch_row_dh<D, 5>(a, grid, s);
+        else if (hpw == 6) launch_row_dh<D, 6>(a, grid, s);
+        else launch_row_dh<D, 7>(a, grid, s);
         break;
       }
       return hipErrorInvalidValue;
@@ -582,7 +598,9 @@ bool row_kernel_supports(int head_dim, int heads_per_wg) {
   const bool d_ok = head_dim == 4 || head_dim == 8 || head_dim == 16 || head_dim == 32 ||
                     head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512;
   const bool h_ok = heads_per_wg == 1 || heads_per_wg == 2 || heads_per_wg == 4 ||
-                    (heads_per_wg == 8 && head_dim <= 256);
+                    (heads_per_wg == 8 && head_dim <= 256) ||
+                    ((heads_per_wg == 3 || (heads_per_wg >= 5 && heads_per_wg <= 7)) &&
+                     row_odd_heads(head_dim));
   return d_ok && h_ok;
 }
 

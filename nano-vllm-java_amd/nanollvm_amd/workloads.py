@@ -194,6 +194,16 @@ def qwen3_decode_large(seed=0, batch=256, lo=128, hi=32768) -> Workload:
                  is_prefill=False, hq=16, hkv=8, d=128, scale=QWEN_SCALE, rng=rng)
 
 
+def qwen3_decode_large_heads(hq, hkv=8, seed=0, batch=256, lo=128, hi=32768) -> Workload:
+    """The headline decode's rows and contexts with another head shape (e.g. Qwen3-14B's 40
+    query heads over 8 KV heads, a GQA ratio of 5)."""
+    rng = np.random.default_rng(seed)
+    ctx = loguniform_lengths(rng, batch, lo, hi)
+    return build(f"decode B={batch} ctx log-U[{lo},{hi}], {hq} q heads / {hkv} KV heads, d=128",
+                 [(c - 1, 1) for c in ctx], is_prefill=False, hq=hq, hkv=hkv, d=128,
+                 scale=QWEN_SCALE, rng=rng)
+
+
 def qwen3_decode_large_share(ways=8, by="head", seed=0, batch=256, lo=128, hi=32768) -> Workload:
     """One GPU's share of the headline decode sharded ``ways`` ways with no exchange: by KV
     head (all rows, 16/ways q heads over 8/ways KV heads) or by sequence (every ways-th row,
