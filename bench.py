@@ -559,6 +559,9 @@ def _extra_builders():
         "c5-chunks-alone": lambda: W.qwen3_4b_mixed(part="chunks"),
         "decode-40q-8kv": lambda: W.qwen3_decode_large_heads(40),
         "decode-56q-8kv": lambda: W.qwen3_decode_large_heads(56),
+        "gemma4-decode-global": W.gemma4_decode_global,
+        "gemma4-decode-global-b256": lambda: W.gemma4_decode_global(batch=256, lo=128,
+                                                                     hi=32768),
         "gemma3-prefill-local": lambda: W.gemma3_prefill(local=True),
         "gemma3-prefill-global": lambda: W.gemma3_prefill(local=False),
         "gemma4-prefill-global": W.gemma4_prefill_global,
@@ -570,7 +573,8 @@ def _extra_builders():
 EXTRA = ["c1-qwen3-decode-b8", "c3-gemma3-decode-local", "c3-gemma3-decode-global",
          "c5-qwen3-4b-mixed", "c5-rows-alone", "c5-chunks-alone", "gemma3-prefill-local",
          "gemma3-prefill-global", "gemma4-prefill-global", "c4-share-head-1of8",
-         "c4-share-seq-1of8", "decode-40q-8kv", "decode-56q-8kv"]
+         "c4-share-seq-1of8", "decode-40q-8kv", "decode-56q-8kv", "gemma4-decode-global",
+         "gemma4-decode-global-b256"]
 
 
 def bench_extra(args, ctx):

@@ -187,6 +187,16 @@ def gemma4_prefill_global(seed=0) -> Workload:
                  d=512, scale=1.0, window=0, rng=rng, rope_theta=1e6, max_pos=32768)
 
 
+def gemma4_decode_global(seed=0, batch=32, lo=512, hi=8192) -> Workload:
+    """The Gemma-4-text global layer's shape (8 q heads / 1 kv head, head dim 512, scale 1.0)
+    in a decode step of ``batch`` rows with log-uniform contexts in [lo, hi]."""
+    rng = np.random.default_rng(seed)
+    ctx = loguniform_lengths(rng, batch, lo, hi)
+    return build(f"gemma4-text global layer decode B={batch} ctx log-U[{lo},{hi}] (8q/1kv, d=512)",
+                 [(c - 1, 1) for c in ctx], is_prefill=False, hq=8, hkv=1, d=512, scale=1.0,
+                 window=0, rng=rng, rope_theta=1e6, max_pos=32768)
+
+
 def qwen3_decode_large(seed=0, batch=256, lo=128, hi=32768) -> Workload:
     rng = np.random.default_rng(seed)
     ctx = loguniform_lengths(rng, batch, lo, hi)
