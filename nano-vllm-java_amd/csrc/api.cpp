@@ -919,13 +919,22 @@ nva_status attention_plan(nva_ctx *ctx, const nva_attn_desc &d, int paged, int b
       *hpw_row = h;
       break;
     }
+  // The MFMA row kernel carries up to 16 heads of one KV head (it is used from 5).
+  if (row_mfma_supports(d.head_dim, paged, block_size))
+    for (int h = std::min(rep, kRowMfmaMaxHeads); h >= kRowMfmaMinHeads; h--)
+      if (rep % h == 0) {
+        if (h > *hpw_row) *hpw_row = h;
+        break;
+      }
   // Query heads per prefill workgroup: at most a quarter of its waves, so a workgroup covers at
   // least 64 queries of each head (measured: Gemma3 d = 256 prefill 13% faster with 2 heads
   // than with 4, Gemma 4 d = 512 3% faster with 1 than with 4, Qwen3-4B shape 4% faster with 2
   // than with 4).
   *hpw_tile = largest_pow2_divisor_upto(rep, prefill_max_heads(d.head_dim));
   const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, *hpw_tile);
-  if (!row_kernel_supports(d.head_dim, *hpw_row))
+  const bool mfma_rows = *hpw_row >= kRowMfmaMinHeads && *hpw_row <= kRowMfmaMaxHeads &&
+                         row_mfma_supports(d.head_dim, paged, block_size);
+  if (!mfma_rows && !row_kernel_supports(d.head_dim, *hpw_row))
     return fail(ctx, NVA_E_UNSUPPORTED, "head_dim %d has no row kernel in this build",
                 d.head_dim);
   PlanKey key;

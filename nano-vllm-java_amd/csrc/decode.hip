@@ -80,6 +80,17 @@ __device__ __forceinline__ float add_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Max and sum over the four lanes {l, l ^ 16, l ^ 32, l ^ 48}; every lane gets the same bits.
+__device__ __forceinline__ float max4_lanes(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float m = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false,
+                                                  false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float sum4_lanes(float x) { return add_xor32(add_xor16(x)); }
+
 // Sum of x over aligned groups of LPT lanes; every lane of the group receives the sum.
 template <int LPT>
 __device__ __forceinline__ float group_sum(float x) {
@@ -411,6 +422,237 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   }
 }
 
+// Split-KV decode with several query heads per KV head on fp32 MFMA (v_mfma_f32_16x16x4_f32),
+// for paged K/V whose pages are a power of two of at least 16 keys, at d = 64 and 128.  The
+// unit of work is the row kernel's: one query row x one key chunk x one KV head x HPW query
+// heads (HPW <= 16); each wave takes 16-key blocks of the chunk in turn (wave w: blocks w,
+// w + 4, ...), so the 4 waves read 64 consecutive keys at a time.
+//   S^T[key][head] = K Q^T  D/4 MFMAs per block: at step s = 4v + c lane (i, g) supplies
+//                           K[t0 + i][16v + 4g + c] (A) and Q[h0 + i][16v + 4g + c] (B, zero
+//                           for i >= HPW), i = lane % 16, g = lane / 16; lane (j, g) then holds
+//                           the scores of head j for keys t0 + 4g + r in st[r];
+//   O^T[dim][head] += V^T P^T  4 x D/16 MFMAs per block: step s contracts key t0 + 4g + s,
+//                           whose probability is this lane's own p[s] (B), against V[that
+//                           key][64w + 4i + c] (A) in block b = 4w + c, so P never leaves the
+//                           registers.
+// Each K load instruction reads 64 contiguous bytes of each of 16 rows and each V load 256
+// contiguous bytes of each of 4 rows (whole 128-byte lines), from a wave-uniform page base plus
+// fixed lane offsets.  The row max needs only the two lane swaps
+// across the lane groups that hold a head; the dot products need no cross-lane reduction, which
+// is what limits the row kernel as the heads per KV head grow.  The MFMA work is the same for
+// any HPW <= 16 (unused columns are zero).
+template <int D>
+__global__ void __launch_bounds__(256) row_mfma_kernel(RowLaunch a, int hpw) {
+  constexpr int DQ = D / 4;   // QK steps per block
+  constexpr int NB = D / 16;  // O^T blocks; block b = 4w + c, row i is dim 64w + 4i + c
+  constexpr int NQ = DQ / 4;  // float4 loads of a K row part per lane
+  constexpr int NV = NB / 4;  // float4 loads of a V row part per lane per key (one per 64 dims)
+  static_assert(NV >= 1, "d >= 64");
+  constexpr int MAXH = kRowMfmaMaxHeads;
+  __shared__ float sm_m[4][MAXH];
+  __shared__ float sm_l[4][MAXH];
+  __shared__ float4 sm_acc[4][MAXH][D / 4];
+  __shared__ int32_t stab[kRowTablePages];
+
+  const int rep = a.hq / a.hkv;
+  const int groups = rep / hpw;
+  const int per_item = a.hkv * groups;
+  const int item = blockIdx.x / per_item;
+  const int gy = blockIdx.x - item * per_item;
+  const RowItem it = a.items[item];
+  const int kvh = gy / groups;
+  const int h0 = kvh * rep + (gy - kvh * groups) * hpw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15;
+  const int g = lane >> 4;
+
+  // B operand of QK: this lane's head i, dims 16v + 4g + [0, 4), pre-scaled to log2 units.
+  const float sl2 = a.scale * 1.4426950408889634f;
+  float q[DQ];
+  if (i < hpw) {
+    const float *qp = a.q + ((size_t)it.qrow * a.hq + h0 + i) * D + 4 * g;
+#pragma unroll
+    for (int v = 0; v < NQ; v++) {
+      const float4 x = ld4(qp + 16 * v);
+      q[4 * v] = x.x * sl2;
+      q[4 * v + 1] = x.y * sl2;
+      q[4 * v + 2] = x.z * sl2;
+      q[4 * v + 3] = x.w * sl2;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < DQ; s++) q[s] = 0.0f;
+  }
+
+  const size_t rs = (size_t)a.hkv * D;
+  const int bs_shift = a.kv.bs_shift;
+  const int blk0 = it.kbeg >> bs_shift;
+  const bool inl = it.blk_a != 0;
+  if (!inl) {
+    const int32_t *table = a.kv.table + (size_t)it.seq * a.kv.bt_stride;
+    const int npages = it.kend > it.kbeg ? ((it.kend - 1) >> bs_shift) - blk0 + 1 : 0;
+    for (int j = threadIdx.x; j < npages; j += blockDim.x) stab[j] = table[blk0 + j];
+    __syncthreads();
+  }
+  const float *kbase_h = a.kv.k + (size_t)kvh * D;
+  const float *vbase_h = a.kv.v + (size_t)kvh * D;
+  const int tfirst = it.kbeg & ~15;
+  // Fixed lane offsets (floats) from a block's first row: K row i, dims 16v + 4g; V rows
+  // 4g + s, dims 64w + 4i.
+  const uint32_t koff = (uint32_t)(i * rs + 4 * g);
+  const uint32_t voff = (uint32_t)(4 * g * rs + 4 * i);
+
+  float kra[DQ], krb[DQ];
+  float vra[4][NB], vrb[4][NB];
+  auto issue = [&](int t0, float(&kr)[DQ], float(&vr)[4][NB]) {
+    // A block past the chunk's end reloads its first block (never folded).
+    const int tb = t0 < it.kend ? t0 : tfirst;
+    const int p = tb >> bs_shift;
+    const int id = inl ? (p == blk0 ? it.blk_a - 1 : it.blk_b)
+                       : __builtin_amdgcn_readfirstlane(stab[p - blk0]);
+    const int64_t row = (int64_t)id * a.kv.block_size + (tb - (p << bs_shift));
+    const float *kb = kbase_h + row * rs;
+    const float *vb = vbase_h + row * rs;
+    uint32_t ko = koff, vo[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) vo[s] = voff + (uint32_t)(s * rs);
+    if (tb < it.kbeg || tb + 16 > it.kend) {
+      // A partial block: every lane reads the block's key nearest its own inside the chunk (an
+      // unwritten slot could hold any bits, NaN included; a finite V row adds 0 at weight 0).
+      const int tk = min(max(tb + i, it.kbeg), it.kend - 1);
+      ko = (uint32_t)((tk - tb) * rs + 4 * g);
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const int tv = min(max(tb + 4 * g + s, it.kbeg), it.kend - 1);
+        vo[s] = (uint32_t)((tv - tb) * rs + 4 * i);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < NQ; v++) {
+      const float4 x = ld4_stream_at(kb, ko + 16 * v);
+      kr[4 * v] = x.x;
+      kr[4 * v + 1] = x.y;
+      kr[4 * v + 2] = x.z;
+      kr[4 * v + 3] = x.w;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const float4 x = ld4_stream_at(vb, vo[s] + 64 * v);
+        vr[s][4 * v] = x.x;
+        vr[s][4 * v + 1] = x.y;
+        vr[s][4 * v + 2] = x.z;
+        vr[s][4 * v + 3] = x.w;
+      }
+  };
+
+  f32x4 o[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) o[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -INFINITY;  // head i's running max (log2 units), the same in its 4 lanes
+  float l_run = 0.0f;       // this lane's part of head i's running sum (its keys 4g + r)
+  auto fold = [&](int t0, const float(&kr)[DQ], const float(&vr)[4][NB]) {
+    f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < DQ; s++) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s], q[s], st, 0, 0, 0);
+    float p[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int key = t0 + 4 * g + r;
+      p[r] = (key >= it.kbeg && key < it.kend) ? st[r] : -INFINITY;
+      mx = fmaxf(mx, p[r]);
+    }
+    mx = max4_lanes(mx);
+    const bool need = mx > m_run + 8.0f;
+    if (__any(need)) {
+      const float mn = need ? mx : m_run;
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mn);
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < NB; b++) o[b] *= alpha;
+      m_run = mn;
+    }
+    const float ms = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      p[r] = __builtin_amdgcn_exp2f(p[r] - ms);
+      l_run += p[r];
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[s][b], p[s], o[b], 0, 0, 0);
+  };
+
+  int t0 = tfirst + 16 * wave;
+  if (t0 < it.kend) {
+    issue(t0, kra, vra);
+    for (;;) {
+      issue(t0 + 64, krb, vrb);
+      fold(t0, kra, vra);
+      t0 += 64;
+      if (t0 >= it.kend) break;
+      issue(t0 + 64, kra, vra);
+      fold(t0, krb, vrb);
+      t0 += 64;
+      if (t0 >= it.kend) break;
+    }
+  }
+
+  // Head i's sum over its 4 lanes; the waves' states merge through LDS.
+  const float l_tot = sum4_lanes(l_run);
+  if (i < hpw) {
+    if (g == 0) {
+      sm_m[wave][i] = m_run;
+      sm_l[wave][i] = l_tot;
+    }
+    // Lane (i, g) holds row 4g + r of block 4w + c: dim 64w + 16g + 4r + c.
+#pragma unroll
+    for (int w = 0; w < NV; w++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        sm_acc[wave][i][16 * w + 4 * g + r] =
+            make_float4(o[4 * w][r], o[4 * w + 1][r], o[4 * w + 2][r], o[4 * w + 3][r]);
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < hpw * (D / 4); idx += blockDim.x) {
+    const int h = idx / (D / 4);
+    const int cc = idx - h * (D / 4);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++) M = fmaxf(M, sm_m[w][h]);
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const float e = __builtin_amdgcn_exp2f(sm_m[w][h] - Ms);
+      L = fmaf(sm_l[w][h], e, L);
+      const float4 x = sm_acc[w][h][cc];
+      A.x = fmaf(x.x, e, A.x);
+      A.y = fmaf(x.y, e, A.y);
+      A.z = fmaf(x.z, e, A.z);
+      A.w = fmaf(x.w, e, A.w);
+    }
+    if (it.part < 0) {
+      const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+      st4(a.out + ((size_t)it.qrow * a.hq + h0 + h) * D + cc * 4,
+          make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv));
+    } else {
+      const size_t pi = (size_t)it.part * a.hq + h0 + h;
+      st4(a.part_acc + pi * D + cc * 4, A);
+      if (cc == 0) {
+        a.part_m[pi] = M;
+        a.part_l[pi] = L;
+      }
+    }
+  }
+}
+
 // Row-wide merge for plans whose split rows have at most MP (4 or 8, kMergeRowsMaxParts)
 // partials (prefill segments): one workgroup per row covers all heads, each thread folding the
 // partials of one float4 of one head in order.  All of a thread's partial loads are issued
@@ -565,6 +807,13 @@ constexpr bool row_odd_heads(int d) { return d >= 32 && d <= 256; }
 template <int D>
 hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
   const dim3 grid(a.num_items * (a.hkv * ((a.hq / a.hkv) / hpw)));
+  if constexpr (D == 64 || D == 128) {
+    if (hpw >= kRowMfmaMinHeads && hpw <= kRowMfmaMaxHeads &&
+        row_mfma_supports(D, a.kv.paged, a.kv.block_size)) {
+      hipLaunchKernelGGL((row_mfma_kernel<D>), grid, dim3(256), 0, s, a, hpw);
+      return hipGetLastError();
+    }
+  }
   switch (hpw) {
     case 1: launch_row_dh<D, 1>(a, grid, s); break;
     case 2: launch_row_dh<D, 2>(a, grid, s); break;
@@ -588,6 +837,11 @@ hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
 }
 
 }  // namespace
+
+bool row_mfma_supports(int head_dim, int paged, int block_size) {
+  return (head_dim == 64 || head_dim == 128) && paged && block_size >= 16 &&
+         (block_size & (block_size - 1)) == 0;
+}
 
 bool row_kernel_supports(int head_dim, int heads_per_wg) {
   const bool d_ok = head_dim == 4 || head_dim == 8 || head_dim == 16 || head_dim == 32 ||

@@ -174,6 +174,13 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream
 bool row_kernel_supports(int head_dim, int heads_per_wg);
 // Most query heads one row-kernel workgroup carries at this head dim (register budget).
 int row_kernel_max_heads(int head_dim);
+// Rows whose workgroups carry kRowMfmaMinHeads..kRowMfmaMaxHeads query heads of one KV head
+// run on the MFMA row kernel where it is built: d = 64 or 128, paged K/V with power-of-two
+// pages of at least 16 tokens.  (From 5 heads per KV head it reads at 6.4-6.5 TB/s for any head
+// count, where the row kernel falls to 5.3 TB/s at 8; at 3-4 heads the row kernel is as fast.)
+constexpr int kRowMfmaMinHeads = 5;
+constexpr int kRowMfmaMaxHeads = 16;
+bool row_mfma_supports(int head_dim, int paged, int block_size);
 bool prefill_kernel_supports(int head_dim, int heads_per_wg);
 // Prefill workgroups that can be resident on one CU at once (occupancy of the kernel), queried
 // on the current device each call (callers cache it per device).

@@ -1,9 +1,11 @@
 """GQA ratios that are not powers of two (query heads per KV head 3, 5, 6, 7: Qwen3-14B has
-40 query heads over 8 KV heads, Qwen2.5-7B 28 over 4), through the C ABI against the oracle:
-decode, paged prefill with prefix hits and one-query rows, and dense prefill, at d = 64 and
-128, page sizes 16 and 256, with and without a sliding window.  The bar is the path's:
-attention within max-abs 1e-4 and rel-L2 1e-5 of the oracle, every page byte equal.
-(Layers/Attention.java:152-171 and :328-396 take any integer ratio: kvh = h / rep.)"""
+40 query heads over 8 KV heads, Qwen2.5-7B 28 over 4) and above 8 (12, 16: the MFMA row kernel
+carries up to 16 heads of a KV head), through the C ABI against the oracle: decode, paged
+prefill with prefix hits and one-query rows, and dense prefill, at d = 64 and 128, page sizes
+16, 256 and 768 (not a power of two: the row kernel instead of the MFMA one), with and without a
+sliding window.  The bar is the path's: attention within max-abs 1e-4 and rel-L2 1e-5 of the
+oracle, every page byte equal.  (Layers/Attention.java:152-171 and :328-396 take any integer
+ratio: kvh = h / rep.)"""
 
 import numpy as np
 import pytest
@@ -34,6 +36,11 @@ CASES = [
     (6, 2, 64, "prefill", 16, 0),
     (5, 1, 64, "dense", 0, 0),
     (7, 2, 128, "dense", 0, 300),
+    (16, 1, 128, "decode", 16, 0),
+    (12, 2, 64, "decode", 256, 33),
+    (16, 2, 128, "prefill", 256, 0),
+    (10, 1, 128, "decode", 768, 0),
+    (8, 2, 128, "decode", 768, 0),
 ]
 
 
