@@ -145,9 +145,14 @@ template <int D, int HPW, bool PAGED_ALIGNED>
 __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   using S = RowShape<D, HPW>;
   constexpr int LPT = S::LPT, VPL = S::VPL, TPW = S::TPW, UH = S::UH, G = S::G;
+  // d = 512 with 8 heads: q lives in LDS (in registers its 64 values per lane left one wave per
+  // SIMD), and the waves' final states merge in two passes of 4 heads to bound the LDS.
+  constexpr bool QL = D >= 512 && HPW >= 8;
+  constexpr int HA = QL ? HPW / 2 : HPW;  // heads per pass of the final merge
   __shared__ float sm_m[4][HPW];
   __shared__ float sm_l[4][HPW];
-  __shared__ float4 sm_acc[4][HPW][D / 4];
+  __shared__ float4 sm_acc[4][HA][D / 4];
+  __shared__ float4 sq[QL ? HPW : 1][QL ? D / 4 : 1];
   __shared__ int32_t stab[kRowTablePages];  // block ids of the pages this item touches
 
   const int rep = a.hq / a.hkv;
@@ -166,14 +171,24 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   // Lane c holds dims [4c + 4*LPT*j, +4) for j < VPL, so each load instruction is contiguous.
   // q is pre-scaled by scale * log2(e): the dot products come out in log2 units.
   const float sl2 = a.scale * 1.4426950408889634f;
-  float4 qv[HPW][VPL];
-#pragma unroll
-  for (int h = 0; h < HPW; h++)
-#pragma unroll
-    for (int j = 0; j < VPL; j++) {
-      const float4 x = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + (c + LPT * j) * 4);
-      qv[h][j] = make_float4(x.x * sl2, x.y * sl2, x.z * sl2, x.w * sl2);
+  float4 qv[QL ? 1 : HPW][VPL];
+  if constexpr (QL) {
+    for (int idx = threadIdx.x; idx < HPW * (D / 4); idx += blockDim.x) {
+      const int h = idx / (D / 4);
+      const int cc = idx - h * (D / 4);
+      const float4 x = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + cc * 4);
+      sq[h][cc] = make_float4(x.x * sl2, x.y * sl2, x.z * sl2, x.w * sl2);
     }
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int h = 0; h < HPW; h++)
+#pragma unroll
+      for (int j = 0; j < VPL; j++) {
+        const float4 x = ld4(a.q + ((size_t)it.qrow * a.hq + h0 + h) * D + (c + LPT * j) * 4);
+        qv[h][j] = make_float4(x.x * sl2, x.y * sl2, x.z * sl2, x.w * sl2);
+      }
+  }
 
   const size_t rs = (size_t)a.hkv * D;
   // Stage the item's block ids in LDS once (the host caps items at kRowTablePages pages), so
@@ -280,21 +295,30 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     }
   };
   auto fold = [&](const float4(&kr)[UH][VPL], const float4(&vr)[UH][VPL], const bool(&ok)[UH]) {
+    // With q in LDS, keep its reads in the loop: hoisted out of it they would take the
+    // registers this layout frees.
+    if constexpr (QL) asm volatile("" ::: "memory");
 #pragma unroll
     for (int h = 0; h < HPW; h++) {
+      float4 qh[VPL];
+#pragma unroll
+      for (int j = 0; j < VPL; j++) {
+        if constexpr (QL) qh[j] = sq[h][c + LPT * j];
+        else qh[j] = qv[h][j];
+      }
       float s[UH];
 #pragma unroll
       for (int u = 0; u < UH; u++) {
-        float p = qv[h][0].x * kr[u][0].x;
-        p = fmaf(qv[h][0].y, kr[u][0].y, p);
-        p = fmaf(qv[h][0].z, kr[u][0].z, p);
-        p = fmaf(qv[h][0].w, kr[u][0].w, p);
+        float p = qh[0].x * kr[u][0].x;
+        p = fmaf(qh[0].y, kr[u][0].y, p);
+        p = fmaf(qh[0].z, kr[u][0].z, p);
+        p = fmaf(qh[0].w, kr[u][0].w, p);
 #pragma unroll
         for (int j = 1; j < VPL; j++) {
-          p = fmaf(qv[h][j].x, kr[u][j].x, p);
-          p = fmaf(qv[h][j].y, kr[u][j].y, p);
-          p = fmaf(qv[h][j].z, kr[u][j].z, p);
-          p = fmaf(qv[h][j].w, kr[u][j].w, p);
+          p = fmaf(qh[j].x, kr[u][j].x, p);
+          p = fmaf(qh[j].y, kr[u][j].y, p);
+          p = fmaf(qh[j].z, kr[u][j].z, p);
+          p = fmaf(qh[j].w, kr[u][j].w, p);
         }
         s[u] = group_sum<LPT>(p);
       }
@@ -374,23 +398,29 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       m[h] = M;
     }
   }
+#pragma unroll
+  for (int pass = 0; pass < HPW / HA; pass++) {
+  if (pass > 0) __syncthreads();  // the previous pass has read sm_acc
   if (sub == 0) {
 #pragma unroll
     for (int h = 0; h < HPW; h++) {
-      if (c == 0) {
+      if (pass == 0 && c == 0) {
         sm_m[wave][h] = m[h];
         sm_l[wave][h] = l[h];
       }
+      if (h / HA == pass) {
 #pragma unroll
-      for (int j = 0; j < VPL; j++) sm_acc[wave][h][c + LPT * j] = acc[h][j];
+        for (int j = 0; j < VPL; j++) sm_acc[wave][h - pass * HA][c + LPT * j] = acc[h][j];
+      }
     }
   }
   __syncthreads();
 
-  // sm_acc[.][h][cc] holds dims [4cc, 4cc + 4) of head h.
-  for (int idx = threadIdx.x; idx < HPW * (D / 4); idx += blockDim.x) {
-    const int h = idx / (D / 4);
-    const int cc = idx - h * (D / 4);
+  // sm_acc[.][h - pass * HA][cc] holds dims [4cc, 4cc + 4) of head h.
+  for (int idx = threadIdx.x; idx < HA * (D / 4); idx += blockDim.x) {
+    const int hl = idx / (D / 4);
+    const int h = pass * HA + hl;
+    const int cc = idx - hl * (D / 4);
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < 4; s++) M = fmaxf(M, sm_m[s][h]);
@@ -401,7 +431,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
     for (int s = 0; s < 4; s++) {
       const float e = __builtin_amdgcn_exp2f(sm_m[s][h] - Ms);
       L = fmaf(sm_l[s][h], e, L);
-      const float4 x = sm_acc[s][h][cc];
+      const float4 x = sm_acc[s][hl][cc];
       A.x = fmaf(x.x, e, A.x);
       A.y = fmaf(x.y, e, A.y);
       A.z = fmaf(x.z, e, A.z);
@@ -420,6 +450,7 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
       }
     }
   }
+  }  // passes
 }
 
 // Split-KV decode with several query heads per KV head on fp32 MFMA (v_mfma_f32_16x16x4_f32),
