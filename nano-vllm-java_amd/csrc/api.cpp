@@ -908,7 +908,7 @@ KvView make_dense_view(const float *k, const float *v) {
 // workgroup of the row and tile kernels.
 nva_status attention_plan(nva_ctx *ctx, const nva_attn_desc &d, int paged, int block_size,
                           int num_blocks, int num_tokens, Plan **plan, int *hpw_row,
-                          int *hpw_tile) {
+                          int *hpw_tile, bool *rows_mfma = nullptr) {
   const int rep = d.num_heads / d.num_kv_heads;
   // Query heads per row workgroup: the largest divisor of the GQA ratio the row kernel is built
   // for, so each K/V byte crosses HBM once per KV head (one head per workgroup at a ratio of 5
@@ -919,21 +919,28 @@ nva_status attention_plan(nva_ctx *ctx, const nva_attn_desc &d, int paged, int b
       *hpw_row = h;
       break;
     }
-  // The MFMA row kernel carries up to 16 heads of one KV head (it is used from 5).
-  if (row_mfma_supports(d.head_dim, paged, block_size))
-    for (int h = std::min(rep, kRowMfmaMaxHeads); h >= kRowMfmaMinHeads; h--)
-      if (rep % h == 0) {
-        if (h > *hpw_row) *hpw_row = h;
-        break;
-      }
   // Query heads per prefill workgroup: at most a quarter of its waves, so a workgroup covers at
   // least 64 queries of each head (measured: Gemma3 d = 256 prefill 13% faster with 2 heads
   // than with 4, Gemma 4 d = 512 3% faster with 1 than with 4, Qwen3-4B shape 4% faster with 2
   // than with 4).
   *hpw_tile = largest_pow2_divisor_upto(rep, prefill_max_heads(d.head_dim));
   const bool mfma = ctx->is_prefill && prefill_kernel_supports(d.head_dim, *hpw_tile);
-  const bool mfma_rows = *hpw_row >= kRowMfmaMinHeads && *hpw_row <= kRowMfmaMaxHeads &&
-                         row_mfma_supports(d.head_dim, paged, block_size);
+  // The MFMA row kernel carries up to 16 heads of one KV head (it is used from 5).  Rows that
+  // run beside MFMA prefill tiles (a mixed step) share the matrix pipes with them: there the row
+  // kernel keeps 5 heads per KV head (40 query heads over 8 KV heads, Qwen3-4B-like mixed step:
+  // attention 1.58-1.60 against 1.67-1.71 ms with MFMA rows), while 8 run as well or better on
+  // MFMA (64 over 8: 2.14-2.25 against 2.25-2.28 ms), the row kernel's 8-head form being slow.
+  bool mfma_rows = false;
+  if (row_mfma_supports(d.head_dim, paged, block_size))
+    for (int h = std::min(rep, kRowMfmaMaxHeads); h >= kRowMfmaMinHeads; h--)
+      if (rep % h == 0) {
+        if (!mfma || *hpw_row != h || h > kRowMfmaMinHeads) {
+          *hpw_row = h;
+          mfma_rows = true;
+        }
+        break;
+      }
+  if (rows_mfma) *rows_mfma = mfma_rows;
   if (!mfma_rows && !row_kernel_supports(d.head_dim, *hpw_row))
     return fail(ctx, NVA_E_UNSUPPORTED, "head_dim %d has no row kernel in this build",
                 d.head_dim);
@@ -1025,8 +1032,9 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
                          Scratch *scr) {
   Plan *plan = nullptr;
   int hpw_row = 0, hpw_tile = 0;
+  bool rows_mfma = false;
   nva_status st = attention_plan(ctx, d, view.paged, view.block_size, num_blocks, num_tokens,
-                                 &plan, &hpw_row, &hpw_tile);
+                                 &plan, &hpw_row, &hpw_tile, &rows_mfma);
   if (st != NVA_OK) return st;
   const int window = d.sliding_window > 0 ? d.sliding_window : 0;
 
@@ -1114,6 +1122,7 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     r.part_m = pm;
     r.part_l = pm + parts;
     r.part_acc = pm + 2 * parts;
+    r.mfma = rows_mfma ? 1 : 0;
     Timed tm(ctx, "decode", row_stream);
     HIP_TRY(ctx, launch_row_attention(r, hpw_row, row_stream), "decode kernel launch");
     tm.done();

@@ -839,7 +839,7 @@ template <int D>
 hipError_t launch_row_d(const RowLaunch &a, int hpw, hipStream_t s) {
   const dim3 grid(a.num_items * (a.hkv * ((a.hq / a.hkv) / hpw)));
   if constexpr (D == 64 || D == 128) {
-    if (hpw >= kRowMfmaMinHeads && hpw <= kRowMfmaMaxHeads &&
+    if (a.mfma && hpw >= 1 && hpw <= kRowMfmaMaxHeads &&
         row_mfma_supports(D, a.kv.paged, a.kv.block_size)) {
       hipLaunchKernelGGL((row_mfma_kernel<D>), grid, dim3(256), 0, s, a, hpw);
       return hipGetLastError();

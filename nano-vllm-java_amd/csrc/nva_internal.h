@@ -75,6 +75,7 @@ struct RowLaunch {
   int32_t hq, hkv, head_dim;
   float scale;
   float *part_m, *part_l, *part_acc;  // [P, Hq], [P, Hq], [P, Hq, D]
+  int32_t mfma = 0;  // the planner chose the MFMA row kernel (row_mfma_supports, 5-16 heads)
 };
 
 struct MergeLaunch {
@@ -174,10 +175,11 @@ hipError_t launch_prefill_tiles(const TileLaunch &a, int heads_per_wg, hipStream
 bool row_kernel_supports(int head_dim, int heads_per_wg);
 // Most query heads one row-kernel workgroup carries at this head dim (register budget).
 int row_kernel_max_heads(int head_dim);
-// Rows whose workgroups carry kRowMfmaMinHeads..kRowMfmaMaxHeads query heads of one KV head
-// run on the MFMA row kernel where it is built: d = 64 or 128, paged K/V with power-of-two
-// pages of at least 16 tokens.  (From 5 heads per KV head it reads at 6.4-6.5 TB/s for any head
-// count, where the row kernel falls to 5.3 TB/s at 8; at 3-4 heads the row kernel is as fast.)
+// The planner gives rows whose workgroups carry kRowMfmaMinHeads..kRowMfmaMaxHeads query heads
+// of one KV head to the MFMA row kernel where it is built: d = 64 or 128, paged K/V with
+// power-of-two pages of at least 16 tokens.  (From 5 heads per KV head it reads at 6.4-6.5 TB/s
+// for any head count, where the row kernel falls to 5.3 TB/s at 8; at 3-4 heads the row kernel
+// is as fast.)  Rows beside MFMA prefill tiles keep the row kernel when it covers the heads.
 constexpr int kRowMfmaMinHeads = 5;
 constexpr int kRowMfmaMaxHeads = 16;
 bool row_mfma_supports(int head_dim, int paged, int block_size);
