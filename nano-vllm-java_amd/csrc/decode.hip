@@ -25,7 +25,9 @@
 //     swaps (no LDS traffic); each group of LPT lanes is an independent online-softmax stream;
 //   * the TPW streams of a wave fold together with lane shuffles, the 4 waves' results merge
 //     through LDS, and either the output row (unsplit item) or the partial (m, l, acc) of the
-//     chunk is written.
+//     chunk is written;
+//   * where the planner gives a workgroup 5 to 16 query heads of one KV head (d = 64 and 128,
+//     power-of-two pages of >= 16 tokens), row_mfma_kernel runs the same units on fp32 MFMA.
 // HBM bytes per work item: chunk * 2 * D * 4 per KV head (+ q, + the partial or output row).
 #include "nva_internal.h"
 #include "nva_device.h"
@@ -468,10 +470,10 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
 //                           registers.
 // Each K load instruction reads 64 contiguous bytes of each of 16 rows and each V load 256
 // contiguous bytes of each of 4 rows (whole 128-byte lines), from a wave-uniform page base plus
-// fixed lane offsets.  The row max needs only the two lane swaps
-// across the lane groups that hold a head; the dot products need no cross-lane reduction, which
-// is what limits the row kernel as the heads per KV head grow.  The MFMA work is the same for
-// any HPW <= 16 (unused columns are zero).
+// fixed lane offsets.  The row max needs only the two lane swaps across the lane groups that
+// hold a head, and the dot products need no cross-lane reduction (the row kernel's reductions
+// grow with the heads per KV head).  The MFMA work is the same for any HPW <= 16 (unused
+// columns are zero).
 template <int D>
 __global__ void __launch_bounds__(256) row_mfma_kernel(RowLaunch a, int hpw) {
   constexpr int DQ = D / 4;   // QK steps per block
@@ -587,7 +589,8 @@ __global__ void __launch_bounds__(256) row_mfma_kernel(RowLaunch a, int hpw) {
   auto fold = [&](int t0, const float(&kr)[DQ], const float(&vr)[4][NB]) {
     f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < DQ; s++) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s], q[s], st, 0, 0, 0);
+    for (int s = 0; s < DQ; s++)
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s], q[s], st, 0, 0, 0);
     float p[4];
     float mx = -INFINITY;
 #pragma unroll
