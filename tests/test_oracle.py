@@ -247,14 +247,18 @@ def test_window_one_returns_own_value():
     assert np.allclose(out[:, 0], vals[:, 0], atol=1e-7)
 
 
-def test_mha_equals_gqa_with_duplicated_kv():
-    rng = np.random.default_rng(9)
+@pytest.mark.parametrize("rep", [2, 3, 5, 7])
+def test_mha_equals_gqa_with_duplicated_kv(rep):
+    # Query head h reads KV head h // rep (Attention.java:152-171): with every KV head repeated
+    # rep times in place, multi-head attention gives the same rows.  The GPU's odd ratios (the
+    # 40 / 8 and 28 / 4 head shapes) are checked against this oracle.
+    rng = np.random.default_rng(9 + rep)
     n = 90
     keys = rng.standard_normal((n, 2, 16), dtype=np.float32)
     vals = rng.standard_normal((n, 2, 16), dtype=np.float32)
-    gqa, q = _single(n, n, 4, 2, 16, keys, vals)
-    mha, _ = _single(n, n, 4, 4, 16, np.repeat(keys, 2, axis=1), np.repeat(vals, 2, axis=1),
-                     q=q)
+    gqa, q = _single(n, n, 2 * rep, 2, 16, keys, vals)
+    mha, _ = _single(n, n, 2 * rep, 2 * rep, 16, np.repeat(keys, rep, axis=1),
+                     np.repeat(vals, rep, axis=1), q=q)
     assert np.max(np.abs(gqa - mha)) < 1e-6
 
 
