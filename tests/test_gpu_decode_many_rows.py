@@ -70,6 +70,7 @@ def test_repeated_calls_bit_identical(ctx):
 
     first = run(big)
     small_first = run(small)
+    assert np.all(np.isfinite(first)) and np.all(np.isfinite(small_first))
     for r in range(3):
         got = run(big)
         say(f"many-row decode repeat {r}: max |got - first| = "

@@ -157,6 +157,7 @@ def run_full_size(ctx, wl, name):
         ctx.bind_kv_cache(b_arena)
         out_b = attn.forward(q, k, v, ctx).cpu().numpy()
         ctx.clear()
+        assert np.all(np.isfinite(out_a))
         assert np.array_equal(bits(out_a), bits(out_b)), "output depends on the block ids"
 
         for arena, slots in ((a_arena, m.slot_mapping), (b_arena, slots_b)):

@@ -80,6 +80,7 @@ def compare(ctx, case, name, mode, theta=1e4, max_pos=512):
         packed = run(ctx, case, rope, norms, packed=True)
     finally:
         rope.close()
+    assert np.all(np.isfinite(split[0]))
     for what, a, b in (("out", split[0], packed[0]), ("rotated q", split[1], packed[1]),
                        ("rotated k", split[2], packed[2])):
         assert np.array_equal(bits(a), bits(b)), f"{what} differs between packed and split"

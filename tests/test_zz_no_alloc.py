@@ -75,6 +75,7 @@ def run_pair(case, name, shared=False):
             ctx.sync()
             assert device_bytes(ctx) > before, "the existing entry point allocates its buffers"
             a, b = out_a.cpu().numpy(), out_b.cpu().numpy()
+            assert np.all(np.isfinite(a))
             say(f"no-alloc {name}: max |a - b| = {float(np.max(np.abs(a - b))):.3e}")
             assert np.array_equal(bits(a), bits(b)), "outputs differ"
             if shared:
