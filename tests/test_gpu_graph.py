@@ -5,10 +5,11 @@ The no-allocation entry point is the one meant for callers under graph capture: 
 plan is in the library's scratch array, a call launches kernels only (no allocation, no plan
 copy, no memset), so its launch sequence can be captured.  Checked on a split-KV decode (store,
 row kernel, merge), on one with more workgroups than the row kernel keeps resident (several
-dispatch rounds), and on a mixed prefill (MFMA tiles on the context's stream, qLen = 1 rows
-forked onto its second stream and joined with events): each replay, with eager work and
-synchronisations between the replays, gives output bit-identical to the eager call on the same
-inputs, also after the inputs the graph reads are overwritten with new values.
+dispatch rounds), on one with 8 query heads per KV head (the MFMA row kernel), and on a mixed
+prefill (MFMA tiles on the context's stream, qLen = 1 rows forked onto its second stream and
+joined with events): each replay, with eager work and synchronisations between the replays,
+gives output bit-identical to the eager call on the same inputs, also after the inputs the graph
+reads are overwritten with new values.
 """
 
 import ctypes
@@ -101,6 +102,17 @@ def test_decode_many_rows_graph_replays():
                         hkv=2, d=64, scale=0.125, rng=rng, block_size=16, pool_cap=1 << 20),
                 seed=43)
     run_graph(case, "decode 1100 rows (several dispatch rounds)", replays=4)
+
+
+def test_decode_mfma_rows_graph_replays():
+    # 64 query heads over 8 KV heads: the rows run on the MFMA row kernel (8 heads per
+    # workgroup).
+    rng = np.random.default_rng(44)
+    ctxs = [int(x) for x in rng.integers(256, 3000, 24)]
+    case = Case(W.build("decode 24 rows, 64 q / 8 kv heads", [(c - 1, 1) for c in ctxs],
+                        is_prefill=False, hq=64, hkv=8, d=128, scale=W.QWEN_SCALE, rng=rng),
+                seed=44)
+    run_graph(case, "decode 24 rows, 64 q / 8 kv heads (MFMA rows)")
 
 
 def test_mixed_step_graph_replays():
