@@ -39,7 +39,19 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps before the timed ones; the part idles at a low clock "
+                         "between phases and takes ~100 back-to-back steps of the prefill "
+                         "(~30 ms) to reach its steady clock (--ramp shows it)")
+    ap.add_argument("--sustain", type=float, default=0.0, metavar="S",
+                    help="after the timed steps, run the step back to back for S seconds and "
+                         "sample the board's socket power and gfx clock every ~10 ms (amdsmi, "
+                         "when importable); the line gains their medians and ms/step after the "
+                         "first 0.5 s")
+    ap.add_argument("--ramp", type=int, default=0, metavar="N",
+                    help="after the timed steps, idle 1 s and then time N back-to-back steps "
+                         "one by one with HIP events; the line gains their mean per range of "
+                         "step indices (the clock transient after the GPU idles)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work budget of the baseline")
@@ -211,7 +223,7 @@ class cu_masked_stream:
 
 
 def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, label,
-              flush=None):
+              flush=None, ramp=0, sustain=0.0):
     import torch
     from nanollvm_amd import Context  # noqa: F401
 
@@ -252,12 +264,120 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
     ms = (t1 - t0) * 1e3 / steps
     log(f"{label}: {ms:.4f} ms/step; kernels " + ", ".join(
         f"{n}={s[1] / max(s[0], 1):.4f}ms x{s[0]}" for n, s in stats.items() if s[0]))
+    ramp_ms = None
+    if ramp > 0:
+        ramp_ms = clock_ramp(step, ramp, flush)
+        log(f"{label}: per-step ms after 1 s idle: " +
+            " ".join(f"[{a}:{b}] {x:.4f}" for a, b, x in ramp_ms))
+    sus = None
+    if sustain > 0:
+        sus = sustained(step, sustain, flush)
+        log(f"{label}: sustained {sus}")
     gms = graph_step_ms(ctx, step, steps, flush)
     if gms is not None:
         log(f"{label}: {gms:.4f} ms/step replaying the step as a HIP graph")
     plan = time_step_plan(ctx, wl, step)
     plan["graph_ms_per_step"] = None if gms is None else round(gms, 5)
+    if ramp_ms is not None:
+        plan["ramp"] = ramp_ms
+    if sus is not None:
+        plan["sustained"] = sus
     return ms, stats, plan
+
+
+def sustained(step, seconds, flush=None):
+    """The step back to back for `seconds` with the board's socket power (W) and gfx clock
+    (MHz) sampled every ~10 ms through amdsmi: medians, the power cap and ms/step over the run
+    after its first 0.5 s (None for the board figures when amdsmi is unavailable)."""
+    import statistics
+    import threading
+    import torch
+    h = cap = None
+    try:
+        import amdsmi
+        amdsmi.amdsmi_init()
+        h = amdsmi.amdsmi_get_processor_handles()[0]
+        cap = amdsmi.amdsmi_get_power_cap_info(h).get("power_cap")
+    except Exception as e:  # no amdsmi module or no access to the board's metrics
+        log(f"board power and clock not sampled: {e}")
+        h = None
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            try:
+                m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+            except Exception:
+                return
+            samples.append((time.time(), m.get("current_socket_power"), m.get("current_gfxclk")))
+            time.sleep(0.01)
+
+    th = threading.Thread(target=sample, daemon=True) if h is not None else None
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    batch = max(1, int(0.05 / max(time.perf_counter() - t, 1e-5)))
+    if th is not None:
+        th.start()
+    t0 = time.time()
+    marks = []
+    n = 0
+    while time.time() - t0 < seconds:
+        for _ in range(batch):
+            if flush is not None:
+                flush()
+            step()
+        torch.cuda.synchronize()
+        n += batch
+        marks.append((time.time(), n))
+    stop.set()
+    if th is not None:
+        th.join()
+        try:
+            amdsmi.amdsmi_shut_down()
+        except Exception:
+            pass
+    w0 = t0 + 0.5
+    first = next((m for m in marks if m[0] >= w0), marks[0])
+    last = marks[-1]
+    ms = (last[0] - first[0]) * 1e3 / max(last[1] - first[1], 1)
+    out = {"seconds": round(last[0] - t0, 2), "steps": last[1], "ms_per_step": round(ms, 5)}
+    win = [x for x in samples if first[0] <= x[0] <= last[0]]
+    pw = [x[1] for x in win if isinstance(x[1], (int, float))]
+    ck = [x[2] for x in win if isinstance(x[2], (int, float))]
+    out["socket_power_w"] = statistics.median(pw) if pw else None
+    out["gfxclk_mhz"] = statistics.median(ck) if ck else None
+    out["power_cap_w"] = round(cap / 1e6) if isinstance(cap, (int, float)) and cap > 0 else None
+    out["samples"] = len(win)
+    return out
+
+
+def clock_ramp(step, n, flush=None, idle_s=1.0):
+    """Per-step HIP-event times of n back-to-back steps started after idle_s seconds with no GPU
+    work: the part drops to a low clock when idle and raises it over the first steps of a
+    load.  Returns [first step, end step, mean ms] per range of step indices."""
+    import torch
+    torch.cuda.synchronize()
+    time.sleep(idle_s)
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    for i in range(n):
+        ev[i].record(s)
+        if flush is not None:
+            flush()
+        step()
+    ev[n].record(s)
+    torch.cuda.synchronize()
+    d = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+    marks = [0, 5, 25, 50, 100, 200, 500, 1000, 2000, 4000, 8000, 16000, 32000]
+    out = []
+    for a, b in zip(marks, marks[1:]):
+        if a >= n:
+            break
+        b = min(b, n)
+        out.append([a, b, round(sum(d[a:b]) / (b - a), 5)])
+    return out
 
 
 def graph_step_ms(ctx, step, steps, flush=None):
@@ -331,7 +451,8 @@ def step_metadata(ctx, wl, plan):
     plan (build, upload); the sum is what a scheduler step pays once, before the kernels of its
     first layer."""
     out = time_step_prepare(ctx, wl)
-    out.update({k: v for k, v in plan.items() if k != "graph_ms_per_step"})
+    out.update({k: v for k, v in plan.items()
+                if k not in ("graph_ms_per_step", "ramp", "sustained")})
     out["per_step_host_us"] = round(out["build_upload_us"] + plan["plans_per_step"] *
                                     (plan["plan_build_us"] + plan["plan_upload_us"]), 1)
     return out
@@ -473,7 +594,8 @@ def bench_decode(args, ctx):
     oq = torch.empty_like(q)
     attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
     ms, stats, plan = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps,
-                                args.warmup, "decode")
+                                args.warmup, "decode", ramp=args.ramp,
+                                sustain=args.sustain)
     byts = decode_bytes(wl)
     n_dec, t_dec = stats["decode"]
     dec_ms = t_dec / max(n_dec, 1)
@@ -490,6 +612,10 @@ def bench_decode(args, ctx):
         "step_metadata": step_metadata(ctx, wl, plan),
         "graph_ms_per_step": plan["graph_ms_per_step"],
     }
+    if "ramp" in plan:
+        res["ramp"] = plan["ramp"]
+    if "sustained" in plan:
+        res["sustained"] = plan["sustained"]
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
     res["o_proj"] = time_o_proj(ctx, attn.forward_with_rope(rope, wl.meta.positions, q, k, v, ctx),
@@ -518,7 +644,8 @@ def bench_prefill(args, ctx):
     attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
     # Paged prefill reads rotated k from the pages, so the rotated k tensor is not requested.
     ms, stats, plan = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps,
-                                args.warmup, "prefill")
+                                args.warmup, "prefill", ramp=args.ramp,
+                                sustain=args.sustain)
     flops = 4.0 * wl.d * wl.hq * wl.visible_pairs()
     n_pf, t_pf = stats["prefill"]
     pf_ms = t_pf / max(n_pf, 1)
@@ -538,6 +665,10 @@ def bench_prefill(args, ctx):
         "step_metadata": step_metadata(ctx, wl, plan),
         "graph_ms_per_step": plan["graph_ms_per_step"],
     }
+    if "ramp" in plan:
+        res["ramp"] = plan["ramp"]
+    if "sustained" in plan:
+        res["sustained"] = plan["sustained"]
     ctx.set(**wl.meta.context_args())
     ctx.bind_kv_cache(arena)
     res["o_proj"] = time_o_proj(ctx, attn.forward_with_rope(rope, wl.meta.positions, q, k, v, ctx),
@@ -601,7 +732,8 @@ def bench_extra(args, ctx):
     junk = torch.empty(512 << 18, device="cuda") if args.flush else None
     flush = (lambda: junk.fill_(1.0)) if args.flush else None
     ms, stats, plan = run_layer(ctx, arena, rope, attn, wl, q, k, v, oq, None, args.steps,
-                                args.warmup, wl.name, flush=flush)
+                                args.warmup, wl.name, flush=flush, ramp=args.ramp,
+                                sustain=args.sustain)
     dec_rows = [(c, n) for c, n in wl.seqs if n == 1]
     pf_rows = [(c, n) for c, n in wl.seqs if n > 1]
     dec_bytes = 0
@@ -631,6 +763,10 @@ def bench_extra(args, ctx):
     line["step_metadata"] = step_metadata(ctx, wl, plan)
     line["attention_ms"] = round(kms.get("attention", 0.0), 5)
     line["graph_ms_per_step"] = plan["graph_ms_per_step"]
+    if "ramp" in plan:
+        line["ramp"] = plan["ramp"]
+    if "sustained" in plan:
+        line["sustained"] = plan["sustained"]
     rope.close()
     arena.close()
     return line
@@ -790,6 +926,10 @@ def main():
             "graph_ms_per_step": dec["graph_ms_per_step"],
             "o_proj": dec["o_proj"],
         })
+        if "ramp" in dec:
+            line["ramp"] = dec["ramp"]
+        if "sustained" in dec:
+            line["sustained"] = dec["sustained"]
     else:
         line.update({"value": pf["tflops"], "unit": "TFLOP/s", "ms_per_step": pf["ms_per_step"],
                      "config": {"workload": pf["workload"]}, "roofline": pf["roofline"]})
