@@ -275,7 +275,7 @@ def run_layer(ctx, arena, rope, attn, wl, q, k, v, out_q, out_k, steps, warmup, 
         log(f"{label}: sustained {sus}")
     gms = graph_step_ms(ctx, step, steps, flush)
     if gms is not None:
-        log(f"{label}: {gms:.4f} ms/step replaying the step as a HIP graph")
+        log(f"{label}: {gms:.4f} ms/step replaying {GRAPH_STEPS} steps per HIP graph")
     plan = time_step_plan(ctx, wl, step)
     plan["graph_ms_per_step"] = None if gms is None else round(gms, 5)
     if ramp_ms is not None:
@@ -380,11 +380,16 @@ def clock_ramp(step, n, flush=None, idle_s=1.0):
     return out
 
 
+GRAPH_STEPS = 10  # layer steps per captured graph
+
+
 def graph_step_ms(ctx, step, steps, flush=None):
-    """The same layer step captured once into a HIP graph (torch.cuda.graph on a side stream the
-    context is switched to) and replayed `steps` times: wall time per replay, or None when the
-    capture fails.  The plan and every buffer already exist from the eager steps, so the
-    captured calls launch kernels only."""
+    """The layer step captured GRAPH_STEPS times into one HIP graph (torch.cuda.graph on a side
+    stream the context is switched to), as an engine captures the layers of a model step
+    together, and the graph replayed until `steps` layer steps have run: wall time per layer
+    step, or None when the capture fails.  With --flush each captured step is preceded by the
+    flush.  The plan and every buffer already exist from the eager steps, so the captured calls
+    launch kernels only."""
     import torch
     s = torch.cuda.Stream()
     ctx.set_stream(s)
@@ -394,18 +399,20 @@ def graph_step_ms(ctx, step, steps, flush=None):
             s.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
-                step()
+                for _ in range(GRAPH_STEPS):
+                    if flush is not None:
+                        flush()
+                    step()
             s.synchronize()
             g.replay()
             s.synchronize()
+            reps = max(1, -(-steps // GRAPH_STEPS))
             t0 = time.perf_counter()
-            for _ in range(steps):  # back to back, like the eager steps
-                if flush is not None:
-                    flush()
+            for _ in range(reps):  # back to back, like the eager steps
                 g.replay()
             s.synchronize()
             total = time.perf_counter() - t0
-        return total * 1e3 / steps
+        return total * 1e3 / (reps * GRAPH_STEPS)
     except RuntimeError as e:
         log(f"graph capture failed: {e}")
         return None
