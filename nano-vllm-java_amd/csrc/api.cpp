@@ -244,6 +244,10 @@ struct nva_ctx {
   DevBuf d_lin;      // split-K partial sums of the linear kernel
   DevBuf d_gather;   // shared-KV gather [2, T, Hkv, d]
 
+  // One word the store / RoPE kernel writes the XCD of its last workgroup to, read by the decode
+  // launch that follows (null if its allocation failed: no rotation).
+  int32_t *xcd_hint = nullptr;
+
   // This device's address of the no-allocation scratch array (null if the lookup failed).
   char *scratch = nullptr;
   hipError_t scratch_err = hipSuccess;
@@ -1123,6 +1127,9 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     r.part_l = pm + parts;
     r.part_acc = pm + 2 * parts;
     r.mfma = rows_mfma ? 1 : 0;
+    r.xcd_hint = ctx->xcd_hint;
+    r.rotate_heads = d.num_kv_heads == 8 && d.head_dim == 128 &&
+                     hpw_row == d.num_heads / d.num_kv_heads;
     Timed tm(ctx, "decode", row_stream);
     HIP_TRY(ctx, launch_row_attention(r, hpw_row, row_stream), "decode kernel launch");
     tm.done();
@@ -1344,6 +1351,12 @@ nva_status nva_ctx_create(int device, nva_ctx **out) {
     return NVA_E_HIP;
   }
   ctx->stream = ctx->own_stream;
+  if (hipMalloc(reinterpret_cast<void **>(&ctx->xcd_hint), 256) != hipSuccess ||
+      hipMemset(ctx->xcd_hint, 0, 256) != hipSuccess) {
+    if (ctx->xcd_hint) (void)hipFree(ctx->xcd_hint);
+    ctx->xcd_hint = nullptr;
+    (void)hipGetLastError();
+  }
   ctx->scratch = scratch_address(device, &ctx->scratch_err);
   *out = ctx;
   return NVA_OK;
@@ -1369,6 +1382,7 @@ nva_status nva_ctx_destroy(nva_ctx *ctx) {
   ctx->d_v_norm.release();
   ctx->d_lin.release();
   ctx->d_gather.release();
+  if (ctx->xcd_hint) (void)hipFree(ctx->xcd_hint);
   (void)hipEventDestroy(ctx->fork_ev);
   (void)hipEventDestroy(ctx->join_ev);
   (void)hipStreamDestroy(ctx->side_stream);
@@ -1752,6 +1766,7 @@ nva_status nva_rope_forward(nva_ctx *ctx, const nva_rope *rope, const float *q, 
   nva_status st = check_positions(ctx, num_tokens, rope->max_pos);
   if (st != NVA_OK) return st;
   RopeStoreLaunch a{};
+  a.xcd_hint = ctx->xcd_hint;
   a.q = q;
   a.k = k;
   a.v = nullptr;
@@ -1796,6 +1811,7 @@ static nva_status attention_forward(nva_ctx *ctx, nva_kv *kv, const nva_attn_des
     st = check_slots(ctx, kv);
     if (st != NVA_OK) return st;
     RopeStoreLaunch a{};
+    a.xcd_hint = ctx->xcd_hint;
     a.q = nullptr;
     a.k = k;
     a.v = v;
@@ -1897,6 +1913,7 @@ static nva_status norm_rope_attention(nva_ctx *ctx, nva_kv *kv, const nva_rope *
     if (st != NVA_OK) return st;
   }
   RopeStoreLaunch a{};
+  a.xcd_hint = ctx->xcd_hint;
   a.q = q;
   a.k = k;
   a.v = v;

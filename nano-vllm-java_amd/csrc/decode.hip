@@ -34,6 +34,20 @@
 
 namespace nva {
 
+// KV head of this workgroup's unit.  Workgroups go to the 8 XCDs in turn, continuing from the
+// launch before, and with 8 units per item each XCD reads one KV head (one 512-byte slice of
+// every 4 KB token row at d = 128).  Measured on the 256-row decode: when each XCD reads the
+// KV heads whose index has the parity of its own id the kernel runs 2.16-2.17 ms, with the
+// other parity 2.22-2.25 ms.  The launch before (kernel (a)) recorded the XCD of its last
+// workgroup, and this launch's first workgroup runs on the next one (checked with per-launch
+// XCD stamps); every workgroup reads the same recorded value and rotates the heads by the same
+// amount, so the units stay a bijection whatever the placement.
+__device__ __forceinline__ int unit_kv_head(const RowLaunch &a, int kvh) {
+  if (!a.rotate_heads || !a.xcd_hint) return kvh;
+  const int first_xcd = (a.xcd_hint[0] + 1) & 7;  // XCD of block 0 under in-turn dispatch
+  return (kvh + (first_xcd & 1)) & 7;              // block b: XCD (b + first_xcd) mod 8
+}
+
 namespace {
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
@@ -163,8 +177,8 @@ __global__ void __launch_bounds__(256) row_attention_kernel(RowLaunch a) {
   const int item = blockIdx.x / per_item;
   const int gy = blockIdx.x - item * per_item;
   const RowItem it = a.items[item];
-  const int kvh = gy / groups;
-  const int h0 = kvh * rep + (gy - kvh * groups) * HPW;
+  const int kvh = unit_kv_head(a, gy / groups);
+  const int h0 = kvh * rep + (gy - (gy / groups) * groups) * HPW;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane / LPT;
@@ -493,8 +507,8 @@ __global__ void __launch_bounds__(256) row_mfma_kernel(RowLaunch a, int hpw) {
   const int item = blockIdx.x / per_item;
   const int gy = blockIdx.x - item * per_item;
   const RowItem it = a.items[item];
-  const int kvh = gy / groups;
-  const int h0 = kvh * rep + (gy - kvh * groups) * hpw;
+  const int kvh = unit_kv_head(a, gy / groups);
+  const int h0 = kvh * rep + (gy - (gy / groups) * groups) * hpw;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15;

@@ -68,4 +68,14 @@ __device__ __forceinline__ void wait_lds_reads() { asm volatile("s_waitcnt lgkmc
 // Workgroup barrier with no implied wait.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Id (0-7) of the XCD this wave runs on (hardware register XCC_ID, bits 3:0).
+__device__ __forceinline__ int xcd_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 7; }
+
+// The launch's last workgroup (in dispatch order) stores the id of its XCD at hint[0].
+__device__ __forceinline__ void record_last_xcd(int32_t *hint) {
+  if (hint && threadIdx.x == 0 && blockIdx.x == gridDim.x - 1 && blockIdx.y == gridDim.y - 1 &&
+      blockIdx.z == gridDim.z - 1)
+    hint[0] = xcd_id();
+}
+
 }  // namespace nva

@@ -76,6 +76,11 @@ struct RowLaunch {
   float scale;
   float *part_m, *part_l, *part_acc;  // [P, Hq], [P, Hq], [P, Hq, D]
   int32_t mfma = 0;  // the planner chose the MFMA row kernel (row_mfma_supports, 5-16 heads)
+  // XCD of the last workgroup of the kernel launched before this one on the stream (written by
+  // that kernel), from which the launch picks the KV head of each workgroup; see xcd_hint in
+  // RopeStoreLaunch.  rotate_heads: 8 KV heads, d = 128, one workgroup per KV head of an item.
+  const int32_t *xcd_hint = nullptr;
+  int32_t rotate_heads = 0;
 };
 
 struct MergeLaunch {
@@ -121,6 +126,11 @@ struct RopeStoreLaunch {
   HeadNorm qn, kn, vn;        // per-head RMSNorm applied to q, k, v before rotation / store
   int32_t iters_per_wg;       // row kernel: row iterations per workgroup (set by the launcher)
   int32_t q_ld, k_ld, v_ld;   // floats per token of the q, k, v inputs (0: hq*d, hk*d, hk*d)
+  // When non-null, the launch's last workgroup writes the id of the XCD it ran on here.  The
+  // hardware hands consecutive workgroups to the 8 XCDs in turn, continuing across launches, so
+  // the next launch's first workgroup lands on the XCD after it; the decode launch that follows
+  // uses that to pair XCDs with KV heads (any value gives the same results).
+  int32_t *xcd_hint;
 };
 
 // Standalone RMSNorm over rows of any width (RMSNorm.forward).

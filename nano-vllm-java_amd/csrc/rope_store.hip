@@ -21,6 +21,7 @@
 // token; every access is a 16-byte vector access when d % 8 == 0 (all shapes of interest),
 // scalar otherwise.
 #include "nva_internal.h"
+#include "nva_device.h"
 
 namespace nva {
 
@@ -89,6 +90,7 @@ __device__ __forceinline__ float partner(float v) {
 
 __global__ void __launch_bounds__(256) rope_store_kernel(RopeStoreLaunch a) {
   extern __shared__ float norm_lds[];  // [rows][d/4] group sums, then [rows] inverse RMS
+  record_last_xcd(a.xcd_hint);
   const int t = blockIdx.x;
   const int d = a.head_dim;
   const int half = d >> 1;
@@ -256,6 +258,7 @@ constexpr int kRopeRowsPerLoad = 4;
 template <int LPR, int VPL>
 __global__ void __launch_bounds__(256) rope_rows_kernel(RopeStoreLaunch a) {
   constexpr int D = 4 * LPR * VPL;
+  record_last_xcd(a.xcd_hint);
   constexpr int HALF = D / 2;
   constexpr int RPB = 256 / LPR;  // row groups per workgroup
   constexpr int NR = kRopeRowsPerLoad;  // rows loaded together

@@ -78,3 +78,40 @@ def test_repeated_calls_bit_identical(ctx):
         assert np.array_equal(bits(got), bits(first)), f"call {r + 2} differs from the first"
         got_small = run(small)
         assert np.array_equal(bits(got_small), bits(small_first)), "small decode differs"
+
+
+def test_decode_bit_identical_under_every_xcd_offset(ctx):
+    """At 8 KV heads and d = 128 the decode launch rotates which KV head each workgroup reads by
+    the XCD the store kernel's last workgroup ran on (workgroups go to the 8 XCDs in turn,
+    continuing across launches).  Calls preceded by 0..7 one-workgroup kernels start on every
+    XCD offset, so both rotations run; every output must be bit-identical to the first."""
+    import torch
+    rng = np.random.default_rng(11)
+    case = Case(W.build("decode 64 rows, 16 q / 8 KV heads", [(int(c) - 1, 1) for c in
+                                                                rng.integers(100, 3000, 64)],
+                        is_prefill=False, hq=16, hkv=8, d=128, scale=0.088388346, rng=rng,
+                        block_size=256, pool_cap=1 << 16), seed=11)
+    wl = case.wl
+    arena = load_arena(ctx, case)
+    tiny = torch.zeros(1, device="cuda")
+    try:
+        ctx.set(**wl.meta.context_args())
+        ctx.bind_kv_cache(arena)
+        attn = Attention(wl.hq, wl.d, wl.scale, wl.hkv, wl.window, 0)
+        q, k, v = dev(case.q), dev(case.k), dev(case.v)
+        first = None
+        for shift in range(8):
+            for _ in range(shift):
+                tiny.add_(1.0)  # one workgroup
+            out = attn.forward(q, k, v, ctx)
+            ctx.sync()
+            got = out.cpu().numpy()
+            if first is None:
+                assert np.all(np.isfinite(got))
+                first = got
+            else:
+                assert np.array_equal(bits(got), bits(first)), f"offset {shift} differs"
+        say("decode bit-identical after 0..7 one-workgroup launches")
+    finally:
+        ctx.clear()
+        arena.close()
