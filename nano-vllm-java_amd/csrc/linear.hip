@@ -426,12 +426,15 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
   }
 }
 
-// Few rows (decode batches): y = x W^T + bias as a weight-streaming GEMV.  Wave w of
-// workgroup b owns output columns n0 = (4b + w) * CPW .. n0 + CPW - 1 for all M rows: lane l
-// reads the 16-byte chunks l, l + 64, ... of those W rows (non-temporal loads: W is read once)
-// and the same chunks of the M x rows (cached: every wave reads them), keeps M * CPW partial
-// dot products, and folds them across the wave in a fixed DPP order.  HBM bytes: W once, plus
-// x and y; the MFMA tiles would compute 128-row blocks for a handful of rows.
+// Few rows (decode batches): y = x W^T + bias as a weight-streaming GEMV.  Workgroup b owns
+// output columns n0 = b * CPW .. n0 + CPW - 1 for all M rows, and its wave w the w-th quarter
+// of K: lane l reads the 16-byte chunks l, l + 64, ... of that quarter of those W rows
+// (non-temporal loads: W is read once) and the same chunks of the M x rows (cached: every
+// workgroup reads them), keeps M * CPW partial dot products, folds them across the wave in a
+// fixed DPP order, and the four quarters are added in wave order through LDS.  With K split,
+// a 2048-wide row takes one round of loads per wave and the grid has four times the waves
+// (8 per CU at 1024 columns), so the latency of the load rounds is paid once.  HBM bytes: W
+// once, plus x and y; the MFMA tiles would compute 128-row blocks for a handful of rows.
 namespace {
 
 typedef float gv4 __attribute__((ext_vector_type(4)));
@@ -456,11 +459,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 template <int M, int CPW>
 __global__ void __launch_bounds__(256) gemv_kernel(LinearLaunch a) {
+  __shared__ float red[4][M][CPW];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int n0 = (blockIdx.x * 4 + wave) * CPW;
-  if (n0 >= a.n) return;  // uniform per wave
+  const int n0 = blockIdx.x * CPW;  // the workgroup's columns; K is split over its 4 waves
   const int chunks = a.k >> 2;
+  const int per = (chunks + 3) >> 2;
+  const int cb = wave * per;
+  const int ce = min(chunks, cb + per);
   float acc[M][CPW];
 #pragma unroll
   for (int m = 0; m < M; m++)
@@ -471,15 +477,16 @@ __global__ void __launch_bounds__(256) gemv_kernel(LinearLaunch a) {
   for (int j = 0; j < CPW; j++) wr[j] = a.w + (size_t)min(n0 + j, a.n - 1) * a.k;
   const int rows = min(M, a.m);
   // U chunks per lane in flight, W and x loads issued together before any arithmetic; chunks
-  // past the end (and x rows past M) load chunk 0 / row 0 and are skipped.
+  // past the wave's range (and x rows past M) load the lane's first chunk / row 0 and are
+  // skipped.
   constexpr int U = M <= 2 ? 4 : 2;
-  for (int c0 = lane; c0 < chunks; c0 += U * 64) {
+  for (int c0 = cb + lane; c0 < ce; c0 += U * 64) {
     float4 wv[U][CPW], xv[U][M];
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      ok[u] = c0 + 64 * u < chunks;
-      const int c = ok[u] ? c0 + 64 * u : 0;
+      ok[u] = c0 + 64 * u < ce;
+      const int c = ok[u] ? c0 + 64 * u : c0;
 #pragma unroll
       for (int j = 0; j < CPW; j++) wv[u][j] = ld4_stream(wr[j] + 4 * c);
 #pragma unroll
@@ -503,14 +510,22 @@ __global__ void __launch_bounds__(256) gemv_kernel(LinearLaunch a) {
       }
     }
   }
+  // Each wave's sums (left in lane 63), then the four K quarters added in wave order.
 #pragma unroll
-  for (int m = 0; m < M; m++) {
-    if (m >= rows) break;
+  for (int m = 0; m < M; m++)
 #pragma unroll
     for (int j = 0; j < CPW; j++) {
       const float t = wave_sum(acc[m][j]);
-      const int n = n0 + j;
-      if (lane == 63 && n < a.n) a.y[(size_t)m * a.n + n] = a.bias ? t + a.bias[n] : t;
+      if (lane == 63) red[wave][m][j] = t;
+    }
+  __syncthreads();
+  if (threadIdx.x < M * CPW) {
+    const int m = threadIdx.x / CPW;
+    const int j = threadIdx.x - m * CPW;
+    const int n = n0 + j;
+    if (m < rows && n < a.n) {
+      const float t = (red[0][m][j] + red[1][m][j]) + (red[2][m][j] + red[3][m][j]);
+      a.y[(size_t)m * a.n + n] = a.bias ? t + a.bias[n] : t;
     }
   }
 }
@@ -519,7 +534,7 @@ int linear_gemv_max_rows() { return 8; }
 
 hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s) {
   constexpr int CPW = 2;
-  const dim3 grid((a.n + 4 * CPW - 1) / (4 * CPW));
+  const dim3 grid((a.n + CPW - 1) / CPW);
   if (a.m <= 1) hipLaunchKernelGGL((gemv_kernel<1, CPW>), grid, dim3(256), 0, s, a);
   else if (a.m <= 2) hipLaunchKernelGGL((gemv_kernel<2, CPW>), grid, dim3(256), 0, s, a);
   else if (a.m <= 4) hipLaunchKernelGGL((gemv_kernel<4, CPW>), grid, dim3(256), 0, s, a);
