@@ -494,7 +494,7 @@ def o_proj_kernel(m, n):
     blocks = ((n + 31) // 32) * ((m + 31) // 32)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if m <= 8:
-        return "gemv_kernel (weight-streaming GEMV, <= 8 rows)"
+        return "gemv_kernel (weight-streaming GEMV, <= 16 rows)"
     if blocks <= cus:
         return "skinny_kernel<8,2> (fp32 MFMA 32x32x2, one 32x32 block per workgroup, K over 8 waves)"
     return "linear_kernel (fp32 MFMA 32x32x2, 128x64 tiles, two workgroups per CU; K slices from a per-CU cost model)"

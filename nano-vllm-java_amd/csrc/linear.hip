@@ -7,7 +7,7 @@
 // result agrees to fp32 rounding (checked against the oracle within the attention tolerance).
 //
 // Mapping onto CDNA4.  Three kernels by shape:
-//   * gemv_kernel for at most 8 rows (a weight-streaming GEMV, below);
+//   * gemv_kernel for at most 16 rows (a weight-streaming GEMV, below);
 //   * skinny_kernel when the 32 x 32 blocks of y number at most one per CU (decode batches of
 //     tens to a few hundred rows): one block per workgroup, K split over its eight waves, each
 //     streaming its own K range through a private LDS ring (below);
@@ -530,7 +530,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(LinearLaunch a) {
   }
 }
 
-int linear_gemv_max_rows() { return 8; }
+int linear_gemv_max_rows() { return 16; }
 
 hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s) {
   constexpr int CPW = 2;
@@ -539,6 +539,7 @@ hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s) {
   else if (a.m <= 2) hipLaunchKernelGGL((gemv_kernel<2, CPW>), grid, dim3(256), 0, s, a);
   else if (a.m <= 4) hipLaunchKernelGGL((gemv_kernel<4, CPW>), grid, dim3(256), 0, s, a);
   else if (a.m <= 8) hipLaunchKernelGGL((gemv_kernel<8, CPW>), grid, dim3(256), 0, s, a);
+  else if (a.m <= 16) hipLaunchKernelGGL((gemv_kernel<16, CPW>), grid, dim3(256), 0, s, a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

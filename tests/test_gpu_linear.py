@@ -67,11 +67,13 @@ def check(got, want, name):
     (2, 4096, 2560, True),     # GEMV path, Qwen3-4B o_proj
     (3, 260, 200, False),      # GEMV path, rows short of its 4-row form, ragged N and K
     (5, 1028, 7, True),        # GEMV path, 8-row form, fewer columns than one workgroup
-    (9, 260, 200, True),       # first row count past the GEMV path (32 x 32 blocks)
+    (9, 260, 200, True),       # GEMV path, 16-row form
+    (16, 2048, 1024, True),    # GEMV path, its largest row count
+    (17, 260, 200, True),      # first row count past the GEMV path (32 x 32 blocks)
     (37, 260, 200, True),      # ragged M, N, K (K % 32 != 0)
     (33, 2048, 1000, True),    # blocks: ragged M and N, K in four slices plus the reduce
     (64, 1028, 1024, True),    # K slices of 288, the last wave's stage 4 k long
-    (16, 8192, 256, False),    # 32 K slices of one 32-k stage per wave
+    (24, 8192, 256, False),    # 32 K slices of one 32-k stage per wave
     (130, 2048, 1024, False),  # M tail past one 128-row tile
     (256, 2048, 1024, True),   # 256-row decode batch: 256 blocks, one per CU
     (384, 2048, 1024, True),   # more blocks than CUs: 128 x 64 tiles, K slices plus the reduce
