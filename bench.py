@@ -492,9 +492,13 @@ def o_proj_kernel(m, n):
     """The library kernel nva_linear_forward runs for an [m, K] x [n, K]^T o_proj."""
     import torch
     blocks = ((n + 31) // 32) * ((m + 31) // 32)
+    blocks16 = ((n + 15) // 16) * ((m + 15) // 16)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if m <= 8:
+    if m <= 16:
         return "gemv_kernel (weight-streaming GEMV, <= 16 rows)"
+    if 2 * blocks <= cus and 2 * blocks16 >= cus and blocks16 <= 2 * cus:
+        return ("skinny16_kernel<8,2> (fp32 MFMA 16x16x4, one 16x16 block per workgroup, "
+                "K over 8 waves)")
     if blocks <= cus:
         return "skinny_kernel<8,2> (fp32 MFMA 32x32x2, one 32x32 block per workgroup, K over 8 waves)"
     return "linear_kernel (fp32 MFMA 32x32x2, 128x64 tiles, two workgroups per CU; K slices from a per-CU cost model)"

@@ -6,8 +6,11 @@
 // output in its gemv panel order; here the sum runs over MFMA steps and split-K slices, so the
 // result agrees to fp32 rounding (checked against the oracle within the attention tolerance).
 //
-// Mapping onto CDNA4.  Three kernels by shape:
+// Mapping onto CDNA4.  Four kernels by shape:
 //   * gemv_kernel for at most 16 rows (a weight-streaming GEMV, below);
+//   * skinny16_kernel when 32 x 32 blocks would fill at most half the CUs but 16 x 16 blocks
+//     fill at least half (tens to ~128 rows at 1024 columns): one 16 x 16 block per
+//     workgroup, K split over its eight waves, no K slices (below);
 //   * skinny_kernel when the 32 x 32 blocks of y number at most one per CU (decode batches of
 //     tens to a few hundred rows): one block per workgroup, K split over its eight waves, each
 //     streaming its own K range through a private LDS ring (below);
@@ -48,6 +51,7 @@
 namespace nva {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -426,6 +430,125 @@ __global__ void __launch_bounds__(64 * NW) skinny_kernel(LinearLaunch a) {
   }
 }
 
+// Decode batches whose 32 x 32 blocks would leave half the CUs idle (tens to ~128 rows at
+// 1024 columns): one 16 x 16 block of y per workgroup on v_mfma_f32_16x16x4_f32, four times the
+// workgroups, so K needs no slices and no reduce launch.  As in skinny_kernel, K is split over
+// the workgroup's NW waves, each streaming its own K range through a private LDS ring (16 x
+// rows and 16 W rows of 32 k per stage, chunk-swizzled), and the waves' blocks are added in
+// wave order through LDS.  Lane (i, g) supplies row i's chunks g and g + 4 of a stage (4 k
+// each) to both operands; MFMA (t, e) contracts component e of chunk g + 4t over g, a k order
+// A and B share.
+template <int NW, int PF>
+__global__ void __launch_bounds__(64 * NW) skinny16_kernel(LinearLaunch a) {
+  constexpr int KI = 32;       // k per stage
+  constexpr int ST = 16 * KI;  // floats per operand per stage
+  constexpr int OPS = 4;       // copy instructions per stage
+  __shared__ __attribute__((aligned(16))) float ring[NW][PF][2][ST];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int kb = blockIdx.z * a.k_per_split;
+  const int ke = min(a.k, kb + a.k_per_split);
+  const int per = (ke - kb + NW * KI - 1) / (NW * KI) * KI;
+  const int wk0 = kb + w * per, wk1 = min(ke, wk0 + per);
+  const int iters = wk1 > wk0 ? (wk1 - wk0 + KI - 1) / KI : 0;
+
+  // Copy instruction c moves rows [8c, 8c + 8) of an operand: lane l takes row 8c + l / 8 (rows
+  // past the edge repeat the last valid row; their sums are not stored), LDS chunk position
+  // l % 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7).  Chunks past the wave's K range are
+  // zeroed at use.
+  const int lrow = lane >> 3, lpos = lane & 7;
+  const int rows_x = min(16, a.m - m0), rows_w = min(16, a.n - n0);
+  uint32_t offx[2], offw[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const int r = 8 * c + lrow;
+    const uint32_t ch = (uint32_t)(lpos ^ ((r >> 1) & 7)) * 16u;
+    offx[c] = (uint32_t)min(r, rows_x - 1) * (uint32_t)a.k * 4u + ch;
+    offw[c] = (uint32_t)min(r, rows_w - 1) * (uint32_t)a.k * 4u + ch;
+  }
+  const uint32_t ring0 = lds_address(&ring[w][0][0][0]);
+  auto issue = [&](int it, int st) __attribute__((always_inline)) {
+    const int kt = wk0 + it * KI;
+    const int cols = min(KI, a.k - kt);  // the descriptors end inside the matrix
+    const float *xb = a.x + (size_t)m0 * a.k + kt;
+    const float *wb = a.w + (size_t)n0 * a.k + kt;
+    const uint32_t dst = ring0 + (uint32_t)(st * 2 * ST) * 4u;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      copy16_to_lds_async(xb, ((rows_x - 1) * a.k + cols) * 4, offx[c], dst + c * 8 * KI * 4);
+      copy16_to_lds_async(wb, ((rows_w - 1) * a.k + cols) * 4, offw[c],
+                          dst + (ST + c * 8 * KI) * 4);
+    }
+  };
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int p = 0; p < PF; p++)
+    if (p < iters) issue(p, p);
+  for (int it = 0; it < iters; it += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+      if (it + p < iters) {
+        if (it + p + PF - 1 < iters)
+          wait_copies<OPS * (PF - 1)>();
+        else
+          wait_copies<0>();
+        const int kt = wk0 + (it + p) * KI;
+        const float *sa = ring[w][p][0], *sb = ring[w][p][1];
+        const int sw = i * KI, sx = (i >> 1) & 7;
+        float4 av[2], bv[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          av[t] = ld4(sa + sw + 4 * ((g + 4 * t) ^ sx));
+          bv[t] = ld4(sb + sw + 4 * ((g + 4 * t) ^ sx));
+        }
+        if (it + p + PF < iters) {
+          wait_lds_reads();  // the refill overwrites this stage
+          issue(it + p + PF, p);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          if (kt + 4 * (g + 4 * t) >= wk1) {
+            av[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+            bv[t] = av[t];
+          }
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t].x, bv[t].x, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t].y, bv[t].y, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t].z, bv[t].z, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t].w, bv[t].w, acc, 0, 0, 0);
+        }
+      }
+    }
+  }
+  // The wave's block goes to its own first stage.  Value r of lane (j, g): row 4g + r, column j.
+  wait_lds_reads();
+  float *red = ring[w][0][0];
+#pragma unroll
+  for (int r = 0; r < 4; r++) red[(4 * g + r) * 16 + i] = acc[r];
+  __syncthreads();
+  for (int u = threadIdx.x; u < 64; u += 64 * NW) {
+    const int row = u >> 2, c = 4 * (u & 3);
+    float4 sacc = ld4(&ring[0][0][0][row * 16 + c]);
+#pragma unroll
+    for (int v = 1; v < NW; v++) {
+      const float4 t = ld4(&ring[v][0][0][row * 16 + c]);
+      sacc.x += t.x;
+      sacc.y += t.y;
+      sacc.z += t.z;
+      sacc.w += t.w;
+    }
+    if (m0 + row >= a.m) continue;
+    float *yr = a.y + (size_t)(m0 + row) * a.n;
+    const float sv[4] = {sacc.x, sacc.y, sacc.z, sacc.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int col = n0 + c + e;
+      if (col < a.n) yr[col] = a.bias ? sv[e] + a.bias[col] : sv[e];
+    }
+  }
+}
+
 // Few rows (decode batches): y = x W^T + bias as a weight-streaming GEMV.  Workgroup b owns
 // output columns n0 = b * CPW .. n0 + CPW - 1 for all M rows, and its wave w the w-th quarter
 // of K: lane l reads the 16-byte chunks l, l + 64, ... of that quarter of those W rows
@@ -571,6 +694,14 @@ hipError_t launch_skinny(const LinearLaunch &a, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   return launch_reduce(a, s);
+}
+
+hipError_t launch_skinny16(const LinearLaunch &a, hipStream_t s) {
+  if (a.m <= 0 || a.n <= 0) return hipSuccess;
+  if (a.splits != 1) return hipErrorInvalidValue;  // one K range per block (no partial planes)
+  const dim3 grid((a.n + 15) / 16, (a.m + 15) / 16, 1);
+  hipLaunchKernelGGL((skinny16_kernel<kSkinnyWaves, 2>), grid, dim3(64 * kSkinnyWaves), 0, s, a);
+  return hipGetLastError();
 }
 
 int linear_tile_rows() { return BM; }

@@ -173,6 +173,8 @@ hipError_t launch_gemv(const LinearLaunch &a, hipStream_t s);
 hipError_t launch_skinny(const LinearLaunch &a, hipStream_t s);
 
 int linear_skinny_waves();
+// 16 x 16 blocks, one per workgroup, K over its waves, no slices (a.splits must be 1).
+hipError_t launch_skinny16(const LinearLaunch &a, hipStream_t s);
 int linear_gemv_max_rows();
 int linear_tile_rows();
 int linear_tile_cols();

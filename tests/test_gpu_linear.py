@@ -71,8 +71,10 @@ def check(got, want, name):
     (16, 2048, 1024, True),    # GEMV path, its largest row count
     (17, 260, 200, True),      # first row count past the GEMV path (32 x 32 blocks)
     (37, 260, 200, True),      # ragged M, N, K (K % 32 != 0)
-    (33, 2048, 1000, True),    # blocks: ragged M and N, K in four slices plus the reduce
-    (64, 1028, 1024, True),    # K slices of 288, the last wave's stage 4 k long
+    (33, 2048, 1000, True),    # 16 x 16 blocks: ragged M and N
+    (100, 2052, 300, False),   # 16 x 16 blocks: ragged M, N and K (K % 32 == 4)
+    (128, 2048, 1024, True),   # 16 x 16 blocks, two per CU (128-row decode batch)
+    (64, 1028, 1024, True),    # 16 x 16 blocks, K of 1028: the last wave's range 4 k long
     (24, 8192, 256, False),    # 32 K slices of one 32-k stage per wave
     (130, 2048, 1024, False),  # M tail past one 128-row tile
     (256, 2048, 1024, True),   # 256-row decode batch: 256 blocks, one per CU
