@@ -292,7 +292,7 @@ nva_status nva_rms_norm_forward(nva_ctx *ctx, const nva_rms_norm *norm, const fl
  * typically the attention output [tokens, num_heads * head_dim] used in place (in < 4194304).
  * fp32 on MFMA; the sum order differs from the reference's gemv panels (fp32 rounding only).
  * Up to 16 rows run the library's weight-streaming GEMV, batches whose 32 x 32 output blocks fit
- * one per CU its block kernel, and larger GEMMs its 128 x 64-tile kernel. */
+ * one per CU its 16 x 16- or 32 x 32-block kernels, and larger GEMMs its 128 x 64-tile kernel. */
 nva_status nva_linear_forward(nva_ctx *ctx, const float *x, int rows, int in,
                               const float *weight, int out, const float *bias, float *y);
 
