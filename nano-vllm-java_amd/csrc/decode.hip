@@ -35,17 +35,22 @@
 namespace nva {
 
 // KV head of this workgroup's unit.  Workgroups go to the 8 XCDs in turn, continuing from the
-// launch before, and with 8 units per item each XCD reads one KV head (one 512-byte slice of
-// every 4 KB token row at d = 128).  Measured on the 256-row decode: when each XCD reads the
-// KV heads whose index has the parity of its own id the kernel runs 2.16-2.17 ms, with the
-// other parity 2.22-2.25 ms.  The launch before (kernel (a)) recorded the XCD of its last
-// workgroup, and this launch's first workgroup runs on the next one (checked with per-launch
-// XCD stamps); every workgroup reads the same recorded value and rotates the heads by the same
-// amount, so the units stay a bijection whatever the placement.
+// launch before, and with 4 or 8 units per item each XCD reads one KV head (a 512-byte slice of
+// every token row at d = 128).  Which parity of head index each XCD should read depends on the
+// kernel (measured at the headline's rows and contexts): the row kernel runs 2.16-2.17 ms at
+// 16 q / 8 KV heads when the head index has the parity of the XCD id and 2.22-2.25 ms with the
+// other (1.098 against 1.133 ms at 8 q / 4 KV heads), the MFMA row kernel the other way round
+// (40 q / 8 KV heads 2.269 against 2.282-2.288 ms, 28 q / 4 KV heads 1.171 against 1.189 ms).
+// The launch before (kernel (a)) recorded the XCD of its last workgroup, and this launch's
+// first workgroup runs on the next one (checked with per-launch XCD stamps); every workgroup
+// reads the same recorded value and rotates the heads by the same amount, so the units stay a
+// bijection whatever the placement.
 __device__ __forceinline__ int unit_kv_head(const RowLaunch &a, int kvh) {
   if (!a.rotate_heads || !a.xcd_hint) return kvh;
   const int first_xcd = (a.xcd_hint[0] + 1) & 7;  // XCD of block 0 under in-turn dispatch
-  return (kvh + (first_xcd & 1)) & 7;              // block b: XCD (b + first_xcd) mod 8
+  // block b: XCD (b + first_xcd) mod 8, and b mod hkv is the unit's KV head before rotation
+  const int r = (first_xcd & 1) ^ (a.mfma ? 1 : 0);
+  return (kvh + r) & (a.hkv - 1);
 }
 
 namespace {

@@ -80,17 +80,21 @@ def test_repeated_calls_bit_identical(ctx):
         assert np.array_equal(bits(got_small), bits(small_first)), "small decode differs"
 
 
-def test_decode_bit_identical_under_every_xcd_offset(ctx):
-    """At 8 KV heads and d = 128 the decode launch rotates which KV head each workgroup reads by
-    the XCD the store kernel's last workgroup ran on (workgroups go to the 8 XCDs in turn,
-    continuing across launches).  Calls preceded by 0..7 one-workgroup kernels start on every
-    XCD offset, so both rotations run; every output must be bit-identical to the first."""
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 4), (40, 8), (28, 4)])
+def test_decode_bit_identical_under_every_xcd_offset(ctx, hq, hkv):
+    """At 4 or 8 KV heads and d = 128 the decode launch rotates which KV head each workgroup
+    reads by the XCD the store kernel's last workgroup ran on (workgroups go to the 8 XCDs in
+    turn, continuing across launches), with the row kernel (2 heads per KV head) and the MFMA
+    row kernel (5 and 7).  Calls preceded by 0..7 one-workgroup kernels start on every XCD
+    offset, so both rotations run; every output must be bit-identical to the first, and the
+    first is checked against the oracle."""
     import torch
-    rng = np.random.default_rng(11)
-    case = Case(W.build("decode 64 rows, 16 q / 8 KV heads", [(int(c) - 1, 1) for c in
-                                                                rng.integers(100, 3000, 64)],
-                        is_prefill=False, hq=16, hkv=8, d=128, scale=0.088388346, rng=rng,
+    rng = np.random.default_rng(11 + hq)
+    case = Case(W.build(f"decode 64 rows, {hq} q / {hkv} KV heads",
+                        [(int(c) - 1, 1) for c in rng.integers(100, 3000, 64)],
+                        is_prefill=False, hq=hq, hkv=hkv, d=128, scale=0.088388346, rng=rng,
                         block_size=256, pool_cap=1 << 16), seed=11)
+    check_attention(ctx, case, f"decode {hq} q / {hkv} KV heads")
     wl = case.wl
     arena = load_arena(ctx, case)
     tiny = torch.zeros(1, device="cuda")
