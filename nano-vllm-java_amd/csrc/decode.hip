@@ -35,11 +35,12 @@
 namespace nva {
 
 // KV head of this workgroup's unit.  Workgroups go to the 8 XCDs in turn, continuing from the
-// launch before, and with 4 or 8 units per item each XCD reads one KV head (a 512-byte slice of
+// launch before, and with 2, 4 or 8 units per item each XCD reads one KV head (a 512-byte slice of
 // every token row at d = 128).  Which parity of head index each XCD should read depends on the
 // kernel (measured at the headline's rows and contexts): the row kernel runs 2.16-2.17 ms at
 // 16 q / 8 KV heads when the head index has the parity of the XCD id and 2.22-2.25 ms with the
-// other (1.098 against 1.133 ms at 8 q / 4 KV heads), the MFMA row kernel the other way round
+// other (1.098 against 1.133 ms at 8 q / 4 KV heads, 0.567 against 0.584 ms at 4 q / 2 KV
+// heads), the MFMA row kernel the other way round
 // (40 q / 8 KV heads 2.269 against 2.282-2.288 ms, 28 q / 4 KV heads 1.171 against 1.189 ms).
 // The launch before (kernel (a)) recorded the XCD of its last workgroup, and this launch's
 // first workgroup runs on the next one (checked with per-launch XCD stamps); every workgroup

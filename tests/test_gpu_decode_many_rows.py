@@ -80,9 +80,9 @@ def test_repeated_calls_bit_identical(ctx):
         assert np.array_equal(bits(got_small), bits(small_first)), "small decode differs"
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 4), (40, 8), (28, 4)])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 4), (4, 2), (40, 8), (28, 4), (10, 2)])
 def test_decode_bit_identical_under_every_xcd_offset(ctx, hq, hkv):
-    """At 4 or 8 KV heads and d = 128 the decode launch rotates which KV head each workgroup
+    """At 2, 4 or 8 KV heads and d = 128 the decode launch rotates which KV head each workgroup
     reads by the XCD the store kernel's last workgroup ran on (workgroups go to the 8 XCDs in
     turn, continuing across launches), with the row kernel (2 heads per KV head) and the MFMA
     row kernel (5 and 7).  Calls preceded by 0..7 one-workgroup kernels start on every XCD
