@@ -1129,7 +1129,8 @@ nva_status run_attention(nva_ctx *ctx, const nva_attn_desc &d, const KvView &vie
     r.mfma = rows_mfma ? 1 : 0;
     r.xcd_hint = ctx->xcd_hint;
     r.rotate_heads = (d.num_kv_heads == 8 || d.num_kv_heads == 4 || d.num_kv_heads == 2) &&
-                     d.head_dim == 128 && hpw_row == d.num_heads / d.num_kv_heads;
+                     (d.head_dim == 128 || d.head_dim == 64) &&
+                     hpw_row == d.num_heads / d.num_kv_heads;
     Timed tm(ctx, "decode", row_stream);
     HIP_TRY(ctx, launch_row_attention(r, hpw_row, row_stream), "decode kernel launch");
     tm.done();

@@ -36,12 +36,15 @@ namespace nva {
 
 // KV head of this workgroup's unit.  Workgroups go to the 8 XCDs in turn, continuing from the
 // launch before, and with 2, 4 or 8 units per item each XCD reads one KV head (a 512-byte slice of
-// every token row at d = 128).  Which parity of head index each XCD should read depends on the
+// every token row at d = 128, 256 bytes at d = 64).  Which parity of head index each XCD should read depends on the
 // kernel (measured at the headline's rows and contexts): the row kernel runs 2.16-2.17 ms at
 // 16 q / 8 KV heads when the head index has the parity of the XCD id and 2.22-2.25 ms with the
 // other (1.098 against 1.133 ms at 8 q / 4 KV heads, 0.567 against 0.584 ms at 4 q / 2 KV
 // heads), the MFMA row kernel the other way round
 // (40 q / 8 KV heads 2.269 against 2.282-2.288 ms, 28 q / 4 KV heads 1.171 against 1.189 ms).
+// At d = 64, where a head's rows start 256 bytes apart instead of 512, both flip (row kernel at
+// 32 q / 8 KV heads 1.129 against 1.158 ms with the other parity, MFMA row kernel at 14 q / 2
+// KV heads 0.319 against 0.323 ms with the same).
 // The launch before (kernel (a)) recorded the XCD of its last workgroup, and this launch's
 // first workgroup runs on the next one (checked with per-launch XCD stamps); every workgroup
 // reads the same recorded value and rotates the heads by the same amount, so the units stay a
@@ -50,7 +53,7 @@ __device__ __forceinline__ int unit_kv_head(const RowLaunch &a, int kvh) {
   if (!a.rotate_heads || !a.xcd_hint) return kvh;
   const int first_xcd = (a.xcd_hint[0] + 1) & 7;  // XCD of block 0 under in-turn dispatch
   // block b: XCD (b + first_xcd) mod 8, and b mod hkv is the unit's KV head before rotation
-  const int r = (first_xcd & 1) ^ (a.mfma ? 1 : 0);
+  const int r = (first_xcd & 1) ^ (a.mfma ? 1 : 0) ^ (a.head_dim == 64 ? 1 : 0);
   return (kvh + r) & (a.hkv - 1);
 }
 

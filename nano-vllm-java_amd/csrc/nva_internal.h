@@ -78,8 +78,8 @@ struct RowLaunch {
   int32_t mfma = 0;  // the planner chose the MFMA row kernel (row_mfma_supports, 5-16 heads)
   // XCD of the last workgroup of the kernel launched before this one on the stream (written by
   // that kernel), from which the launch picks the KV head of each workgroup; see xcd_hint in
-  // RopeStoreLaunch.  rotate_heads: 2, 4 or 8 KV heads, d = 128, one workgroup per KV head of
-  // an item.
+  // RopeStoreLaunch.  rotate_heads: 2, 4 or 8 KV heads, d = 64 or 128, one workgroup per KV
+  // head of an item.
   const int32_t *xcd_hint = nullptr;
   int32_t rotate_heads = 0;
 };

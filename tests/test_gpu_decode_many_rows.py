@@ -80,9 +80,10 @@ def test_repeated_calls_bit_identical(ctx):
         assert np.array_equal(bits(got_small), bits(small_first)), "small decode differs"
 
 
-@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 4), (4, 2), (40, 8), (28, 4), (10, 2)])
-def test_decode_bit_identical_under_every_xcd_offset(ctx, hq, hkv):
-    """At 2, 4 or 8 KV heads and d = 128 the decode launch rotates which KV head each workgroup
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (8, 4, 128), (4, 2, 128), (40, 8, 128),
+                                      (28, 4, 128), (10, 2, 128), (32, 8, 64), (14, 2, 64)])
+def test_decode_bit_identical_under_every_xcd_offset(ctx, hq, hkv, d):
+    """At 2, 4 or 8 KV heads and d = 64 or 128 the decode launch rotates which KV head each workgroup
     reads by the XCD the store kernel's last workgroup ran on (workgroups go to the 8 XCDs in
     turn, continuing across launches), with the row kernel (2 heads per KV head) and the MFMA
     row kernel (5 and 7).  Calls preceded by 0..7 one-workgroup kernels start on every XCD
@@ -90,11 +91,11 @@ def test_decode_bit_identical_under_every_xcd_offset(ctx, hq, hkv):
     first is checked against the oracle."""
     import torch
     rng = np.random.default_rng(11 + hq)
-    case = Case(W.build(f"decode 64 rows, {hq} q / {hkv} KV heads",
+    case = Case(W.build(f"decode 64 rows, {hq} q / {hkv} KV heads, d={d}",
                         [(int(c) - 1, 1) for c in rng.integers(100, 3000, 64)],
-                        is_prefill=False, hq=hq, hkv=hkv, d=128, scale=0.088388346, rng=rng,
-                        block_size=256, pool_cap=1 << 16), seed=11)
-    check_attention(ctx, case, f"decode {hq} q / {hkv} KV heads")
+                        is_prefill=False, hq=hq, hkv=hkv, d=d, scale=float(1.0 / np.sqrt(d)),
+                        rng=rng, block_size=256, pool_cap=1 << 16), seed=11)
+    check_attention(ctx, case, f"decode {hq} q / {hkv} KV heads, d={d}")
     wl = case.wl
     arena = load_arena(ctx, case)
     tiny = torch.zeros(1, device="cuda")
